@@ -1,0 +1,267 @@
+"""Benchmark of the MI355X activation path (one GPU).
+
+Metric: achieved HBM TB/s and fraction of the 8 TB/s peak per
+op. A "step" is one launch of an op over one batch of synthetic input that is
+already resident in HBM. Each op is timed over exactly --steps launches
+captured in one HIP graph (so host-side validation and launch latency are not
+in the window), bracketed by torch.cuda.synchronize() and HIP events on the
+stream the kernels run on. Every launch of a timed run uses a different set of
+input/output buffers, rotating over enough sets that the working set is
+>= 2 GiB, so no step can be served from the 256 MB Infinity Cache left warm by
+the previous one.
+
+The headline `value` is the BASELINE config-2 workload (fused RMSNorm +
+residual, bf16 [8192, 4096]); every other config's op is reported under "ops".
+Achieved bandwidth = algorithmic bytes per launch / average launch duration.
+
+The CPU baseline (rank 0, N=1) times the CPU oracle - the torch-CPU
+restatement of the reference's eager op (baselines/rmsnorm_residual.py) - on a
+bounded sample of the same workload on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_GBPS = 8000.0
+ROTATE_BYTES = 2 << 30
+
+
+def _parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--ops", default="all", help="comma-separated op names, or 'all'")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline time budget")
+    return p.parse_args()
+
+
+def _ensure_built():
+    from custom_cuda_kernals_amd import build
+
+    if not build.is_built():
+        build.build_all()
+
+
+class Op:
+    """One benchmarked op: a buffer-set factory, a launch on set i, algorithmic bytes."""
+
+    def __init__(self, name, workload, nbytes, make_set, launch, set_bytes):
+        self.name, self.workload, self.nbytes = name, workload, nbytes
+        self.make_set, self.launch, self.set_bytes = make_set, launch, set_bytes
+
+
+def _ops(torch, native):
+    dev = "cuda"
+    bf16 = torch.bfloat16
+    f8 = torch.float8_e4m3fn
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rn(*shape, dtype=bf16):
+        return torch.randn(shape, device=dev, dtype=torch.float32, generator=g).to(dtype)
+
+    ops = []
+
+    # 1: per-token FP8, X [2048, 4096] bf16 with 0.1 % outliers x50
+    m1, n1 = 2048, 4096
+
+    def mk1():
+        x = rn(m1, n1)
+        idx = torch.randperm(m1 * n1, device=dev, generator=g)[: round(0.001 * m1 * n1)]
+        x.view(-1)[idx] *= 50
+        return dict(x=x, q=torch.empty(m1, n1, dtype=f8, device=dev), s=torch.empty(m1, device=dev))
+
+    ops.append(Op("fp8_quant_token", "fp8_token_bf16_2048x4096", m1 * n1 * 3 + m1 * 4, mk1,
+                  lambda b: native.fp8_quant_token_fwd(b["x"], b["q"], b["s"], "e4m3"), m1 * n1 * 3))
+
+    # 2: RMSNorm + residual, [8192, 4096] bf16, eps 1e-5
+    m2, n2 = 8192, 4096
+    w2 = (1.0 + 0.1 * torch.randn(n2, device=dev, generator=g)).to(bf16)
+
+    def mk2():
+        return dict(x=rn(m2, n2), r=rn(m2, n2), y=torch.empty(m2, n2, dtype=bf16, device=dev),
+                    ro=torch.empty(m2, n2, dtype=bf16, device=dev))
+
+    ops.append(Op("rmsnorm_residual", "rmsnorm_residual_bf16_8192x4096", m2 * n2 * 8 + n2 * 2, mk2,
+                  lambda b: native.rmsnorm_residual_fwd(b["x"], b["r"], w2, b["y"], b["ro"], 1e-5), m2 * n2 * 8))
+
+    # 3 / 3v: SwiGLU [8192, 14336] bf16, and SwiGLU + per-token FP8
+    m3, n3 = 8192, 14336
+
+    def mk3():
+        return dict(g=rn(m3, n3), u=rn(m3, n3), y=torch.empty(m3, n3, dtype=bf16, device=dev),
+                    q=torch.empty(m3, n3, dtype=f8, device=dev), s=torch.empty(m3, device=dev))
+
+    ops.append(Op("swiglu", "swiglu_bf16_8192x14336", m3 * n3 * 6, mk3,
+                  lambda b: native.swiglu_fwd(b["g"], b["u"], b["y"]), m3 * n3 * 6))
+    ops.append(Op("swiglu_fp8_token", "swiglu_fp8_token_bf16_8192x14336", m3 * n3 * 5 + m3 * 4, mk3,
+                  lambda b: native.swiglu_fp8_fwd(b["g"], b["u"], b["q"], b["s"], "e4m3", None), m3 * n3 * 5))
+
+    # 4: RoPE in place, q [8,4096,32,128], k [8,4096,8,128] bf16, theta 5e5
+    B, S, HQ, HKV, D = 8, 4096, 32, 8, 128
+    inv = 1.0 / (500000.0 ** (torch.arange(0, D, 2, dtype=torch.float32, device=dev) / D))
+    ang = torch.outer(torch.arange(S, dtype=torch.float32, device=dev), inv)
+    cos4, sin4 = ang.cos().contiguous(), ang.sin().contiguous()
+    rope_elems = B * S * (HQ + HKV) * D
+
+    def mk4():
+        return dict(q=rn(B, S, HQ, D), k=rn(B, S, HKV, D))
+
+    ops.append(Op("rope_inplace", "rope_bf16_q8x4096x32x128_k8x4096x8x128", rope_elems * 4 + 2 * S * (D // 2) * 4, mk4,
+                  lambda b: native.rope_fwd(b["q"], b["k"], cos4, sin4, b["q"], b["k"]), rope_elems * 4))
+
+    # 5a / 5b: T = 16384 chain, per-token and static 0.05
+    m5, n5a, n5b = 16384, 4096, 14336
+    w5 = (1.0 + 0.1 * torch.randn(n5a, device=dev, generator=g)).to(bf16)
+
+    def mk5a():
+        return dict(x=rn(m5, n5a), r=rn(m5, n5a), q=torch.empty(m5, n5a, dtype=f8, device=dev),
+                    ro=torch.empty(m5, n5a, dtype=bf16, device=dev), s=torch.empty(m5, device=dev))
+
+    def mk5b():
+        return dict(g=rn(m5, n5b), u=rn(m5, n5b), q=torch.empty(m5, n5b, dtype=f8, device=dev),
+                    s=torch.empty(m5, device=dev))
+
+    e5a, e5b = m5 * n5a, m5 * n5b
+    ops.append(Op("rmsnorm_residual_fp8_token", "chain_rmsnorm_fp8_token_bf16_16384x4096",
+                  e5a * 7 + m5 * 4 + n5a * 2, mk5a,
+                  lambda b: native.rmsnorm_residual_fp8_fwd(b["x"], b["r"], w5, b["q"], b["s"], b["ro"], 1e-5, "e4m3", None),
+                  e5a * 7))
+    ops.append(Op("swiglu_fp8_token_T16384", "chain_swiglu_fp8_token_bf16_16384x14336", e5b * 5 + m5 * 4, mk5b,
+                  lambda b: native.swiglu_fp8_fwd(b["g"], b["u"], b["q"], b["s"], "e4m3", None), e5b * 5))
+    ops.append(Op("rmsnorm_residual_fp8_static", "chain_rmsnorm_fp8_static0.05_bf16_16384x4096",
+                  e5a * 7 + n5a * 2, mk5a,
+                  lambda b: native.rmsnorm_residual_fp8_fwd(b["x"], b["r"], w5, b["q"], None, b["ro"], 1e-5, "e4m3", 0.05),
+                  e5a * 7))
+    ops.append(Op("swiglu_fp8_static_T16384", "chain_swiglu_fp8_static0.05_bf16_16384x14336", e5b * 5, mk5b,
+                  lambda b: native.swiglu_fp8_fwd(b["g"], b["u"], b["q"], None, "e4m3", 0.05), e5b * 5))
+    return ops
+
+
+def _time_op(torch, op, steps, warmup):
+    nsets = max(2, math.ceil(ROTATE_BYTES / op.set_bytes))
+    sets = [op.make_set() for _ in range(nsets)]
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        op.launch(sets[i % nsets])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(steps):
+                op.launch(sets[i % nsets])
+    torch.cuda.current_stream().wait_stream(side)
+    graph.replay()  # untimed replay: first replay uploads the graph
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    us = ms * 1000.0 / steps
+    gbps = op.nbytes / (us * 1e-6) / 1e9
+    del graph, sets
+    torch.cuda.empty_cache()
+    return {"workload": op.workload, "us": round(us, 3), "GB_per_s": round(gbps, 1),
+            "frac_of_8TBps": round(gbps / PEAK_GBPS, 4), "algorithmic_bytes": op.nbytes,
+            "steps": steps, "buffer_sets": nsets, "total_ms": round(ms, 4)}
+
+
+def _cpu_baseline(budget_s: float):
+    """Time the CPU oracle's RMSNorm+residual (torch-CPU eager restatement) on
+    a bounded row sample of the config-2 workload."""
+    import torch
+
+    from oracle import eager, inputs
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rows, cols = 1024, 4096
+    x, r, w = inputs.rmsnorm_inputs(rows, cols, torch.bfloat16, seed=0)
+    for _ in range(2):
+        eager.rmsnorm_residual(x, r, w, 1e-5)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter_ns()
+        eager.rmsnorm_residual(x, r, w, 1e-5)
+        times.append(time.perf_counter_ns() - t0)
+    times.sort()
+    med_s = times[len(times) // 2] * 1e-9
+    nbytes = rows * cols * 8 + cols * 2
+    return {"value": round(nbytes / med_s / 1e12, 6), "unit": "TB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"oracle eager rmsnorm_residual on bf16 [{rows},{cols}] rows of the config-2 workload, "
+                      f"median of {len(times)} runs over ~{budget_s:.0f}s, {med_s * 1e3:.3f} ms/run"}
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                          "(multi-GPU sharding is design-only, see DESIGN.md)"}))
+        sys.exit(2)
+
+    import torch
+
+    _ensure_built()
+    from custom_cuda_kernals_amd._lib import native
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+
+    ops = _ops(torch, native)
+    wanted = None if args.ops == "all" else set(args.ops.split(","))
+    results = {}
+    for op in ops:
+        if wanted and op.name not in wanted:
+            continue
+        results[op.name] = _time_op(torch, op, args.steps, args.warmup)
+        print(f"# {op.name}: {results[op.name]}", file=sys.stderr, flush=True)
+
+    head = results.get("rmsnorm_residual") or next(iter(results.values()))
+    head_name = "rmsnorm_residual" if "rmsnorm_residual" in results else next(iter(results))
+    achieved = head["GB_per_s"]
+    line = {
+        "metric": "achieved HBM TB/s & % of 8 TB/s peak per op (FP8 quant, RMSNorm, SwiGLU, RoPE)",
+        "value": round(achieved / 1000.0, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us"] / 1000.0, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs generated on the GPU, resident in HBM)",
+        "config": {"workload": head["workload"], "op": head_name, "global_batch": 8192, "seq_len": 1,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBPS, 4), "traffic": None},
+        "ops": results,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = _cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,105 @@
+"""Build recipe for the in-tree native artefacts (gfx950 only).
+
+* ``libcustom_kernels_amd.so`` - the HIP kernels behind the C ABI declared in
+  ``include/custom_kernels_amd.h`` (hipcc, ``--offload-arch=gfx950``).
+* ``_native.<abi>.so`` - the pybind11 validating binding (g++), linked to the
+  library above through the C ABI only, found at run time via ``$ORIGIN``.
+
+Both land next to this file so they travel with the source tree. Run as
+``python -m custom_cuda_kernals_amd.build``.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+import sysconfig
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "libcustom_kernels_amd.so"
+HIP_SOURCES = ["fp8_quant.hip", "rmsnorm_residual.hip", "swiglu.hip", "rope.hip", "selftest.hip"]
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+HIP_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # Products and sums are rounded separately unless a kernel writes an fma.
+    "-ffp-contract=off",
+    # Keep hand-written fp32 code scalar (no v_pk_{add,mul,fma}_f32).
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+    f"-I{ROOT / 'include'}",
+]
+
+
+def native_ext_path() -> Path:
+    suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    return PKG / f"_native{suffix}"
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        line for line in proc.stdout.splitlines()
+        if "packed-fp32-ops' is not a recognized feature" not in line
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out, file=sys.stderr)
+
+
+def build_library() -> Path:
+    BUILD.mkdir(exist_ok=True)
+    objs = [BUILD / (src.replace(".hip", ".o")) for src in HIP_SOURCES]
+    cmds = [
+        [HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+        for src, obj in zip(HIP_SOURCES, objs)
+    ]
+    with cf.ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 4)) as ex:
+        list(ex.map(_run, cmds))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_native() -> Path:
+    import pybind11
+
+    out = native_ext_path()
+    tmp = out.with_suffix(".tmp")
+    _run([
+        "g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall",
+        f"-I{pybind11.get_include()}",
+        f"-I{sysconfig.get_paths()['include']}",
+        str(CSRC / "native.cpp"),
+        f"-L{PKG}", "-lcustom_kernels_amd",
+        "-Wl,-rpath,$ORIGIN",
+        "-o", str(tmp),
+    ])
+    os.replace(tmp, out)
+    return out
+
+
+def build_all() -> None:
+    build_library()
+    build_native()
+
+
+def is_built() -> bool:
+    return LIB.exists() and native_ext_path().exists()
+
+
+if __name__ == "__main__":
+    build_all()
+    print(f"built {LIB.name} and {native_ext_path().name}")

@@ -1,0 +1,377 @@
+// Dynamic and static FP8 quantisation for gfx950.
+//
+// Semantics (baselines/fp8_quant.py:162-189): scale = clamp(amax / FP8_MAX,
+// min=1e-12); codes = (x.float() / scale).to(fp8). Four granularities:
+//
+//   token  - one scale per row ([M]); not in the reference, it is
+//            eager_fp8_quant's "tensor" formula applied to each row;
+//   block  - one scale per 128x128 tile (fp8_quant.cu:59-152 in the reference);
+//   tensor - one dynamic scale for the matrix (fp8_quant.cu:159-234);
+//   static - a caller-given scale, no reduction.
+//
+// Design: a row (token mode) or tile (block mode) is read from HBM once with
+// 16-byte loads and kept in registers while the workgroup reduces |x| with
+// integer max on the magnitude bits (NaN-propagating, like torch's max); the
+// division by the scale is the three-op correctly rounded form
+// (div_by_scale) and the conversion is v_cvt_pk_fp8/bf8_f32. Rows or tiles
+// whose scale is non-finite, or whose quotients leave the verified range of
+// the hardware conversion, take the exact path (x86-compatible division +
+// software encoder) as a workgroup-uniform branch.
+#include "launch.hpp"
+
+namespace cck {
+namespace {
+
+// Store VEC fp8 bytes (4 or 8) at byte offset `off` of `q` (VEC-aligned).
+template <int VEC>
+__device__ inline void store_codes(uint8_t* q, int64_t off, const uint32_t (&w)[VEC / 4]) {
+  if constexpr (VEC == 8) {
+    *reinterpret_cast<u32x2*>(q + off) = (u32x2){w[0], w[1]};
+  } else {
+    *reinterpret_cast<uint32_t*>(q + off) = w[0];
+  }
+}
+
+template <class C, int FMT>
+__device__ inline void quant_vec(const u32x4& raw, float s, float r, bool fast, uint8_t* q, int64_t off) {
+  float f[C::VEC];
+  C::unpack(raw, f);
+  uint32_t w[C::VEC / 4];
+  if (fast) {
+    quant_fast<FMT, C::VEC>(f, s, r, w);
+  } else {
+    quant_exact<FMT, C::VEC>(f, s, w);
+  }
+  store_codes<C::VEC>(q, off, w);
+}
+
+template <int FMT>
+__device__ inline uint8_t quant1(float v, float s, float r, bool fast) {
+  if (fast) {
+    return (uint8_t)(Fp8<FMT>::cvt4(div_by_scale(v, s, r), 0.0f, 0.0f, 0.0f) & 0xffu);
+  }
+  return (uint8_t)Fp8<FMT>::encode(div_x86(v, s));
+}
+
+template <class C>
+struct AmaxOp {
+  using type = MaxPkU16;
+};
+template <>
+struct AmaxOp<CodecF32> {
+  using type = MaxU32;
+};
+
+// ---------------------------------------------------------------------------
+// Token granularity, register-resident rows: one workgroup per row, each
+// thread holds ITEMS 16-byte vectors. Requires cols % VEC == 0 and 16-byte
+// aligned x, VEC-aligned q.
+// ---------------------------------------------------------------------------
+template <class C, int FMT, int THREADS, int ITEMS>
+__global__ __launch_bounds__(THREADS) void fp8_token_resident(const void* __restrict__ x,
+                                                              uint8_t* __restrict__ q,
+                                                              float* __restrict__ scale,
+                                                              int64_t rows, int64_t cols) {
+  constexpr int NW = THREADS / 64;
+  __shared__ uint32_t lds[2 * NW];
+  const int nvec = (int)(cols / C::VEC);
+  int parity = 0;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const u32x4* xr =
+        reinterpret_cast<const u32x4*>(static_cast<const char*>(x) + row * cols * C::kBytes);
+    u32x4 raw[ITEMS];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+      const int v = threadIdx.x + k * THREADS;
+      if (v < nvec) {
+        raw[k] = __builtin_nontemporal_load(xr + v);
+        acc = C::absmax_vec(raw[k], acc);
+      }
+    }
+    acc = block_allreduce<NW>(acc, typename AmaxOp<C>::type{}, lds, parity);
+    parity ^= 1;
+    const float amax = C::absmax_to_float(acc);
+    const float s = scale_from_amax<FMT>(amax);
+    const float r = 1.0f / s;
+    if (threadIdx.x == 0) scale[row] = s;
+    const bool fast = fast_path_ok<FMT>(s, r, amax);
+    uint8_t* qr = q + row * cols;
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+      const int v = threadIdx.x + k * THREADS;
+      if (v < nvec) quant_vec<C, FMT>(raw[k], s, r, fast, qr, (int64_t)v * C::VEC);
+    }
+  }
+}
+
+// Token granularity, any alignment / row length: scalar loads, the row is
+// read twice (the second read is served by L2 for rows up to a few MB).
+template <class C, int FMT>
+__global__ __launch_bounds__(256) void fp8_token_generic(const void* __restrict__ x,
+                                                         uint8_t* __restrict__ q,
+                                                         float* __restrict__ scale, int64_t rows,
+                                                         int64_t cols) {
+  __shared__ uint32_t lds[2 * 4];
+  int parity = 0;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const int64_t base = row * cols;
+    uint32_t acc = 0;
+    for (int64_t j = threadIdx.x; j < cols; j += 256) acc = C::absmax1(x, base + j, acc);
+    acc = block_allreduce<4>(acc, typename AmaxOp<C>::type{}, lds, parity);
+    parity ^= 1;
+    const float amax = C::absmax_to_float(acc);
+    const float s = scale_from_amax<FMT>(amax);
+    const float r = 1.0f / s;
+    if (threadIdx.x == 0) scale[row] = s;
+    const bool fast = fast_path_ok<FMT>(s, r, amax);
+    for (int64_t j = threadIdx.x; j < cols; j += 256) {
+      q[base + j] = quant1<FMT>(C::load1(x, base + j), s, r, fast);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Block granularity: one 256-thread workgroup per 128x128 tile, tile kept in
+// registers. Vector path needs n % VEC == 0 and aligned pointers.
+// ---------------------------------------------------------------------------
+constexpr int kTile = 128;
+
+template <class C, int FMT>
+__global__ __launch_bounds__(256) void fp8_block_resident(const void* __restrict__ x,
+                                                          uint8_t* __restrict__ q,
+                                                          float* __restrict__ scale, int64_t m,
+                                                          int64_t n) {
+  constexpr int VPR = kTile / C::VEC;  // vectors per tile row
+  constexpr int RPP = 256 / VPR;       // tile rows per pass
+  constexpr int ITEMS = kTile / RPP;
+  __shared__ uint32_t lds[2 * 4];
+  const int cv = threadIdx.x % VPR;
+  const int rr = threadIdx.x / VPR;
+  const int64_t col = (int64_t)blockIdx.x * kTile + cv * C::VEC;
+  const int64_t row0 = (int64_t)blockIdx.y * kTile + rr;
+  const bool col_ok = col < n;
+  u32x4 raw[ITEMS];
+  uint32_t acc = 0;
+#pragma unroll
+  for (int k = 0; k < ITEMS; ++k) {
+    const int64_t row = row0 + k * RPP;
+    if (col_ok && row < m) {
+      raw[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          static_cast<const char*>(x) + (row * n + col) * C::kBytes));
+      acc = C::absmax_vec(raw[k], acc);
+    }
+  }
+  acc = block_allreduce<4>(acc, typename AmaxOp<C>::type{}, lds, 0);
+  const float amax = C::absmax_to_float(acc);
+  const float s = scale_from_amax<FMT>(amax);
+  const float r = 1.0f / s;
+  if (threadIdx.x == 0) scale[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = s;
+  const bool fast = fast_path_ok<FMT>(s, r, amax);
+#pragma unroll
+  for (int k = 0; k < ITEMS; ++k) {
+    const int64_t row = row0 + k * RPP;
+    if (col_ok && row < m) quant_vec<C, FMT>(raw[k], s, r, fast, q, row * n + col);
+  }
+}
+
+template <class C, int FMT>
+__global__ __launch_bounds__(256) void fp8_block_generic(const void* __restrict__ x,
+                                                         uint8_t* __restrict__ q,
+                                                         float* __restrict__ scale, int64_t m,
+                                                         int64_t n) {
+  __shared__ uint32_t lds[2 * 4];
+  const int64_t r0 = (int64_t)blockIdx.y * kTile, c0 = (int64_t)blockIdx.x * kTile;
+  const int64_t rh = (m - r0 < kTile) ? m - r0 : kTile;
+  const int64_t cw = (n - c0 < kTile) ? n - c0 : kTile;
+  uint32_t acc = 0;
+  for (int64_t t = threadIdx.x; t < rh * cw; t += 256) {
+    acc = C::absmax1(x, (r0 + t / cw) * n + c0 + t % cw, acc);
+  }
+  acc = block_allreduce<4>(acc, typename AmaxOp<C>::type{}, lds, 0);
+  const float amax = C::absmax_to_float(acc);
+  const float s = scale_from_amax<FMT>(amax);
+  const float r = 1.0f / s;
+  if (threadIdx.x == 0) scale[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = s;
+  const bool fast = fast_path_ok<FMT>(s, r, amax);
+  for (int64_t t = threadIdx.x; t < rh * cw; t += 256) {
+    const int64_t i = (r0 + t / cw) * n + c0 + t % cw;
+    q[i] = quant1<FMT>(C::load1(x, i), s, r, fast);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tensor granularity: amax pass (atomicMax of the non-negative float bits into
+// a caller-zeroed int32, as the reference ABI prescribes), then a flat cast
+// pass that also serves static scales.
+// ---------------------------------------------------------------------------
+template <class C, bool VECTOR>
+__global__ __launch_bounds__(256) void fp8_tensor_amax(const void* __restrict__ x, int64_t total,
+                                                       int32_t* __restrict__ amax_bits) {
+  __shared__ uint32_t lds[2 * 4];
+  uint32_t acc = 0;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if constexpr (VECTOR) {
+    const int64_t nvec = total / C::VEC;
+    const u32x4* xv = static_cast<const u32x4*>(x);
+    for (int64_t v = tid; v < nvec; v += stride) acc = C::absmax_vec(__builtin_nontemporal_load(xv + v), acc);
+    for (int64_t i = nvec * C::VEC + tid; i < total; i += stride) acc = C::absmax1(x, i, acc);
+  } else {
+    for (int64_t i = tid; i < total; i += stride) acc = C::absmax1(x, i, acc);
+  }
+  acc = block_allreduce<4>(acc, typename AmaxOp<C>::type{}, lds, 0);
+  if (threadIdx.x == 0) atomicMax(amax_bits, (int32_t)f32_bits(C::absmax_to_float(acc)));
+}
+
+// STATIC: scale is `static_scale`; otherwise it derives from *amax_bits and is
+// written to scale_out[0].
+template <class C, int FMT, bool STATIC, bool VECTOR>
+__global__ __launch_bounds__(256) void fp8_tensor_cast(const void* __restrict__ x,
+                                                       uint8_t* __restrict__ q,
+                                                       float* __restrict__ scale_out,
+                                                       const int32_t* __restrict__ amax_bits,
+                                                       float static_scale, int64_t total) {
+  float s, amax_t = 0.0f;
+  if constexpr (STATIC) {
+    s = static_scale;
+  } else {
+    amax_t = bits_f32((uint32_t)*amax_bits);
+    s = scale_from_amax<FMT>(amax_t);
+    if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
+  }
+  const float r = 1.0f / s;
+  const bool fast_t = fast_path_ok<FMT>(s, r, amax_t);
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  int64_t done = 0;
+  if constexpr (VECTOR) {
+    const int64_t nvec = total / C::VEC;
+    const u32x4* xv = static_cast<const u32x4*>(x);
+    for (int64_t v = tid; v < nvec; v += stride) {
+      const u32x4 raw = __builtin_nontemporal_load(xv + v);
+      bool fast = fast_t;
+      if constexpr (STATIC) fast = fast_path_ok<FMT>(s, r, C::absmax_to_float(C::absmax_vec(raw, 0)));
+      quant_vec<C, FMT>(raw, s, r, fast, q, v * C::VEC);
+    }
+    done = nvec * C::VEC;
+  }
+  for (int64_t i = done + tid; i < total; i += stride) {
+    const float v = C::load1(x, i);
+    bool fast = fast_t;
+    if constexpr (STATIC) fast = fast_path_ok<FMT>(s, r, __builtin_fabsf(v));
+    q[i] = quant1<FMT>(v, s, r, fast);
+  }
+}
+
+// Row-length buckets of the register-resident token kernel.
+template <class C, int FMT>
+int32_t launch_token(const void* x, uint8_t* q, float* scale, int64_t m, int64_t n,
+                     hipStream_t st) {
+  const bool vec_ok = (n % C::VEC == 0) && host_aligned(x, 16) && host_aligned(q, C::VEC);
+  const int64_t nvec = n / C::VEC;
+  const unsigned g = row_grid(m);
+  if (vec_ok && nvec <= 64) {
+    fp8_token_resident<C, FMT, 64, 1><<<g, 64, 0, st>>>(x, q, scale, m, n);
+  } else if (vec_ok && nvec <= 256) {
+    fp8_token_resident<C, FMT, 256, 1><<<g, 256, 0, st>>>(x, q, scale, m, n);
+  } else if (vec_ok && nvec <= 512) {
+    fp8_token_resident<C, FMT, 256, 2><<<g, 256, 0, st>>>(x, q, scale, m, n);
+  } else if (vec_ok && nvec <= 1024) {
+    fp8_token_resident<C, FMT, 256, 4><<<g, 256, 0, st>>>(x, q, scale, m, n);
+  } else if (vec_ok && nvec <= 2048) {
+    fp8_token_resident<C, FMT, 256, 8><<<g, 256, 0, st>>>(x, q, scale, m, n);
+  } else if (vec_ok && nvec <= 4096) {
+    fp8_token_resident<C, FMT, 512, 8><<<g, 512, 0, st>>>(x, q, scale, m, n);
+  } else {
+    fp8_token_generic<C, FMT><<<g, 256, 0, st>>>(x, q, scale, m, n);
+  }
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace cck
+
+using namespace cck;
+
+extern "C" int32_t launch_fp8_quant_token_fwd(const void* x, uint8_t* x_fp8, float* scale, int64_t m,
+                                              int64_t n, int32_t dtype, int32_t fp8_format,
+                                              void* stream) {
+  if (m <= 0 || n <= 0) return (int32_t)hipSuccess;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_codec(dtype, [&](auto codec) {
+    using C = decltype(codec);
+    return with_fp8(fp8_format, [&](auto f) {
+      return launch_token<C, decltype(f)::value>(x, x_fp8, scale, m, n, st);
+    });
+  });
+}
+
+extern "C" int32_t launch_fp8_quant_block_fwd(const void* x, uint8_t* x_fp8, float* scale, int64_t m,
+                                              int64_t n, int32_t dtype, int32_t fp8_format,
+                                              void* stream) {
+  if (m <= 0 || n <= 0) return (int32_t)hipSuccess;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t nrb = (m + kTile - 1) / kTile, ncb = (n + kTile - 1) / kTile;
+  if (nrb > 65535 || ncb > (int64_t)0x7fffffff) return (int32_t)hipErrorInvalidValue;
+  const dim3 grid((unsigned)ncb, (unsigned)nrb);
+  return with_codec(dtype, [&](auto codec) {
+    using C = decltype(codec);
+    return with_fp8(fp8_format, [&](auto f) {
+      constexpr int FMT = decltype(f)::value;
+      const bool vec_ok = (n % C::VEC == 0) && host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
+      if (vec_ok) {
+        fp8_block_resident<C, FMT><<<grid, 256, 0, st>>>(x, x_fp8, scale, m, n);
+      } else {
+        fp8_block_generic<C, FMT><<<grid, 256, 0, st>>>(x, x_fp8, scale, m, n);
+      }
+      return launch_status();
+    });
+  });
+}
+
+extern "C" int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, float* scale,
+                                               int32_t* amax_scratch, int64_t m, int64_t n,
+                                               int32_t dtype, int32_t fp8_format, void* stream) {
+  if (m <= 0 || n <= 0) return (int32_t)hipSuccess;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t total = m * n;
+  return with_codec(dtype, [&](auto codec) {
+    using C = decltype(codec);
+    return with_fp8(fp8_format, [&](auto f) {
+      constexpr int FMT = decltype(f)::value;
+      const bool vec_ok = host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
+      const unsigned g = flat_grid(total / C::VEC, 256, 2048);
+      if (vec_ok) {
+        fp8_tensor_amax<C, true><<<g, 256, 0, st>>>(x, total, amax_scratch);
+        fp8_tensor_cast<C, FMT, false, true><<<g, 256, 0, st>>>(x, x_fp8, scale, amax_scratch, 0.0f, total);
+      } else {
+        fp8_tensor_amax<C, false><<<g, 256, 0, st>>>(x, total, amax_scratch);
+        fp8_tensor_cast<C, FMT, false, false><<<g, 256, 0, st>>>(x, x_fp8, scale, amax_scratch, 0.0f, total);
+      }
+      return launch_status();
+    });
+  });
+}
+
+extern "C" int32_t launch_fp8_quant_static_fwd(const void* x, uint8_t* x_fp8, float scale, int64_t m,
+                                               int64_t n, int32_t dtype, int32_t fp8_format,
+                                               void* stream) {
+  if (m <= 0 || n <= 0) return (int32_t)hipSuccess;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t total = m * n;
+  return with_codec(dtype, [&](auto codec) {
+    using C = decltype(codec);
+    return with_fp8(fp8_format, [&](auto f) {
+      constexpr int FMT = decltype(f)::value;
+      const bool vec_ok = host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
+      const unsigned g = flat_grid(total / C::VEC, 256, 8192);
+      if (vec_ok) {
+        fp8_tensor_cast<C, FMT, true, true><<<g, 256, 0, st>>>(x, x_fp8, nullptr, nullptr, scale, total);
+      } else {
+        fp8_tensor_cast<C, FMT, true, false><<<g, 256, 0, st>>>(x, x_fp8, nullptr, nullptr, scale, total);
+      }
+      return launch_status();
+    });
+  });
+}

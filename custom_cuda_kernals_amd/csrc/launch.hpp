@@ -1,0 +1,55 @@
+// Host-side helpers shared by the launchers: dtype / format dispatch and the
+// error convention of the C ABI (0 == hipSuccess; hipErrorInvalidValue for an
+// unknown tag, returned before any device call; the launch status otherwise).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "cdna4.hpp"
+#include "../../include/custom_kernels_amd.h"
+
+namespace cck {
+
+template <int V>
+using IntC = std::integral_constant<int, V>;
+
+template <class Fn>
+inline int32_t with_codec(int32_t dtype, Fn&& fn) {
+  switch (dtype) {
+    case kF32: return fn(CodecF32{});
+    case kF16: return fn(CodecF16{});
+    case kBF16: return fn(CodecBF16{});
+    default: return (int32_t)hipErrorInvalidValue;
+  }
+}
+
+template <class Fn>
+inline int32_t with_fp8(int32_t fmt, Fn&& fn) {
+  switch (fmt) {
+    case kF8E4M3: return fn(IntC<kF8E4M3>{});
+    case kF8E5M2: return fn(IntC<kF8E5M2>{});
+    default: return (int32_t)hipErrorInvalidValue;
+  }
+}
+
+inline int32_t launch_status() { return (int32_t)hipGetLastError(); }
+
+inline bool host_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Grid size for row-per-workgroup kernels: one workgroup per row up to the
+// grid limit; kernels loop over rows beyond it.
+inline unsigned row_grid(int64_t rows) {
+  const int64_t cap = 1 << 30;
+  return (unsigned)(rows < cap ? rows : cap);
+}
+
+inline unsigned flat_grid(int64_t work_items, int threads, int64_t cap) {
+  int64_t g = (work_items + threads - 1) / threads;
+  if (g < 1) g = 1;
+  return (unsigned)(g < cap ? g : cap);
+}
+
+}  // namespace cck

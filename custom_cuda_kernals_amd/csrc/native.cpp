@@ -1,0 +1,439 @@
+// custom_cuda_kernals_amd._native: the validating binding layer between the
+// Python API and the C ABI of libcustom_kernels_amd.so.
+//
+// It restates the observable behaviour of the reference's Rust/PyO3 module
+// `custom_cuda._native` (src/lib.rs:11-29, src/kernels/*.rs) in C++:
+//   * the same function names and positional arguments, returning None;
+//   * the same per-tensor checks in the same order (device type "cuda" ->
+//     contiguity -> dtype tag), read through the same Python attributes
+//     (device.type, is_contiguous(), str(dtype), data_ptr(), device.index,
+//     shape) - src/kernels/tensor.rs:38-121;
+//   * the same error mapping: validation failures raise ValueError,
+//     a non-zero launcher status raises RuntimeError
+//     (src/kernels/error.rs:9-36);
+//   * launches on torch.cuda.current_stream(device_index).cuda_stream
+//     (src/kernels/rmsnorm_residual.rs:87-94); no synchronisation.
+// It does not link against torch: it only calls Python attributes, exactly as
+// the reference does, and talks to the kernels through the C ABI.
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <cstdint>
+#include <optional>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../../include/custom_kernels_amd.h"
+
+namespace py = pybind11;
+
+namespace {
+
+enum Tag : int32_t { F32 = 0, F16 = 1, BF16 = 2, F8E4M3 = 3, F8E5M2 = 4 };
+
+const char* tag_debug(int32_t t) {
+  switch (t) {
+    case F32: return "F32";
+    case F16: return "F16";
+    case BF16: return "BF16";
+    case F8E4M3: return "F8E4M3";
+    case F8E5M2: return "F8E5M2";
+    default: return "?";
+  }
+}
+
+std::optional<int32_t> tag_from_dtype_str(const std::string& s) {
+  if (s == "torch.float32") return F32;
+  if (s == "torch.float16") return F16;
+  if (s == "torch.bfloat16") return BF16;
+  if (s == "torch.float8_e4m3fn") return F8E4M3;
+  if (s == "torch.float8_e5m2") return F8E5M2;
+  return std::nullopt;
+}
+
+std::string shape_str(const std::vector<int64_t>& v) {
+  std::ostringstream o;
+  o << "[";
+  for (size_t i = 0; i < v.size(); ++i) o << (i ? ", " : "") << v[i];
+  o << "]";
+  return o.str();
+}
+
+[[noreturn]] void value_error(const std::string& msg) { throw py::value_error(msg); }
+[[noreturn]] void shape_mismatch(const std::string& msg) { value_error("shape mismatch: " + msg); }
+[[noreturn]] void unsupported_dtype(const std::string& what) {
+  value_error("unsupported dtype '" + what + "'; expected float32, float16, or bfloat16");
+}
+
+struct RawView {
+  uintptr_t ptr;
+  int64_t device_index;
+  std::vector<int64_t> shape;
+  std::string dtype_str;
+};
+
+struct View {
+  uintptr_t ptr;
+  int32_t dtype;
+  int64_t device_index;
+  std::vector<int64_t> shape;
+};
+
+RawView validate_and_extract(const char* name, const py::handle& obj) {
+  py::object device = obj.attr("device");
+  const std::string device_type = py::str(device.attr("type"));
+  if (device_type != "cuda") {
+    value_error(std::string("argument '") + name + "' must be a CUDA tensor, got device type '" +
+                device_type + "'");
+  }
+  if (!obj.attr("is_contiguous")().cast<bool>()) {
+    value_error(std::string("argument '") + name + "' must be contiguous");
+  }
+  RawView v;
+  v.dtype_str = py::str(obj.attr("dtype"));
+  v.ptr = obj.attr("data_ptr")().cast<uintptr_t>();
+  v.device_index = device.attr("index").cast<int64_t>();
+  for (py::handle d : obj.attr("shape")) v.shape.push_back(d.cast<int64_t>());
+  return v;
+}
+
+View validate_tensor(const char* name, const py::handle& obj) {
+  RawView r = validate_and_extract(name, obj);
+  auto tag = tag_from_dtype_str(r.dtype_str);
+  if (!tag) unsupported_dtype(r.dtype_str);
+  return View{r.ptr, *tag, r.device_index, std::move(r.shape)};
+}
+
+View validate_int32_tensor(const char* name, const py::handle& obj) {
+  RawView r = validate_and_extract(name, obj);
+  if (r.dtype_str != "torch.int32") {
+    unsupported_dtype(std::string(name) + " must be int32, got " + r.dtype_str);
+  }
+  return View{r.ptr, -1, r.device_index, std::move(r.shape)};
+}
+
+void check_dtype_matches(const char* name, const View& v, const View& expected, const char* ref) {
+  if (v.dtype != expected.dtype) {
+    value_error(std::string("dtype mismatch: '") + name + "' is " + tag_debug(v.dtype) +
+                " but expected " + tag_debug(expected.dtype) + " (must match '" + ref + "')");
+  }
+}
+
+void* current_stream(int64_t device_index) {
+  py::object torch = py::module_::import("torch");
+  py::object stream = torch.attr("cuda").attr("current_stream")(device_index);
+  return reinterpret_cast<void*>(stream.attr("cuda_stream").cast<uintptr_t>());
+}
+
+void check_launch(const char* launcher, int32_t err) {
+  if (err != 0) {
+    throw std::runtime_error(std::string("HIP error: ") + launcher + " failed, hipError_t = " +
+                             std::to_string(err));
+  }
+}
+
+int64_t product(const std::vector<int64_t>& v, size_t begin, size_t end) {
+  int64_t p = 1;
+  for (size_t i = begin; i < end; ++i) p *= v[i];
+  return p;
+}
+
+int32_t parse_fp8_format(const std::string& f) {
+  if (f == "e4m3") return F8E4M3;
+  if (f == "e5m2") return F8E5M2;
+  value_error("fp8_format must be 'e4m3' or 'e5m2', got \"" + f + "\"");
+}
+
+void require_f32(const char* what, const View& v) {
+  if (v.dtype != F32) {
+    unsupported_dtype(std::string(what) + " must be float32, got " + tag_debug(v.dtype));
+  }
+}
+
+void require_fp8_out(const View& v, int32_t fmt, const std::string& fmt_str, const char* name) {
+  if (v.dtype != fmt) {
+    unsupported_dtype(std::string(name) + " dtype " + tag_debug(v.dtype) +
+                      " does not match requested fp8_format \"" + fmt_str + "\"");
+  }
+}
+
+// ---- reference functions (src/lib.rs:13-15,26-27) -------------------------
+
+// src/kernels/rmsnorm_residual.rs:46-115
+void rmsnorm_residual_fwd(py::handle x, py::handle residual, py::handle weight, py::handle y,
+                          py::handle residual_out, double eps) {
+  View xv = validate_tensor("x", x);
+  View rv = validate_tensor("residual", residual);
+  View wv = validate_tensor("weight", weight);
+  View yv = validate_tensor("y", y);
+  View rov = validate_tensor("residual_out", residual_out);
+  check_dtype_matches("residual", rv, xv, "x");
+  check_dtype_matches("weight", wv, xv, "x");
+  check_dtype_matches("y", yv, xv, "x");
+  check_dtype_matches("residual_out", rov, xv, "x");
+  if (rv.shape != xv.shape || yv.shape != xv.shape || rov.shape != xv.shape) {
+    shape_mismatch("x/residual/y/residual_out must share the same shape; got x=" + shape_str(xv.shape) +
+                   ", residual=" + shape_str(rv.shape) + ", y=" + shape_str(yv.shape) +
+                   ", residual_out=" + shape_str(rov.shape));
+  }
+  if (xv.shape.empty()) shape_mismatch("x must have at least 1 dimension");
+  const int64_t cols = xv.shape.back();
+  if (wv.shape != std::vector<int64_t>{cols}) {
+    shape_mismatch("weight shape " + shape_str(wv.shape) + " must be [" + std::to_string(cols) +
+                   "] (x's last dimension)");
+  }
+  const int64_t rows = product(xv.shape, 0, xv.shape.size() - 1);
+  void* st = current_stream(xv.device_index);
+  check_launch("launch_rmsnorm_residual_fwd",
+               launch_rmsnorm_residual_fwd((const void*)xv.ptr, (const void*)rv.ptr, (const void*)wv.ptr,
+                                           (void*)yv.ptr, (void*)rov.ptr, rows, cols, (float)eps,
+                                           xv.dtype, st));
+}
+
+// src/kernels/swiglu.rs:31-79
+void swiglu_fwd(py::handle gate, py::handle up, py::handle y) {
+  View gv = validate_tensor("gate", gate);
+  View uv = validate_tensor("up", up);
+  View yv = validate_tensor("y", y);
+  check_dtype_matches("up", uv, gv, "x");
+  check_dtype_matches("y", yv, gv, "x");
+  if (uv.shape != gv.shape || yv.shape != gv.shape) {
+    shape_mismatch("gate/up/y must share the same shape; got gate=" + shape_str(gv.shape) +
+                   ", up=" + shape_str(uv.shape) + ", y=" + shape_str(yv.shape));
+  }
+  const int64_t n = product(gv.shape, 0, gv.shape.size());
+  void* st = current_stream(gv.device_index);
+  check_launch("launch_swiglu_fwd", launch_swiglu_fwd((const void*)gv.ptr, (const void*)uv.ptr,
+                                                      (void*)yv.ptr, n, gv.dtype, st));
+}
+
+// src/kernels/rope.rs:42-153
+void rope_fwd(py::handle q, py::handle k, py::handle cos, py::handle sin, py::handle q_out,
+              py::handle k_out) {
+  View qv = validate_tensor("q", q);
+  View kv = validate_tensor("k", k);
+  View cv = validate_tensor("cos", cos);
+  View sv = validate_tensor("sin", sin);
+  View qov = validate_tensor("q_out", q_out);
+  View kov = validate_tensor("k_out", k_out);
+  check_dtype_matches("k", kv, qv, "x");
+  check_dtype_matches("q_out", qov, qv, "x");
+  check_dtype_matches("k_out", kov, kv, "x");
+  if (cv.dtype != F32) {
+    unsupported_dtype(std::string("cos must be float32 (RoPE tables are always fp32), got ") + tag_debug(cv.dtype));
+  }
+  if (sv.dtype != F32) {
+    unsupported_dtype(std::string("sin must be float32 (RoPE tables are always fp32), got ") + tag_debug(sv.dtype));
+  }
+  if (qv.shape.size() != 4) {
+    shape_mismatch("q must be 4-D [batch, seq_len, n_q_heads, head_dim], got " + shape_str(qv.shape));
+  }
+  if (kv.shape.size() != 4) {
+    shape_mismatch("k must be 4-D [batch, seq_len, n_kv_heads, head_dim], got " + shape_str(kv.shape));
+  }
+  if (qov.shape != qv.shape) shape_mismatch("q_out must match q's shape");
+  if (kov.shape != kv.shape) shape_mismatch("k_out must match k's shape");
+  const int64_t batch = qv.shape[0], seq_len = qv.shape[1], n_q_heads = qv.shape[2], head_dim = qv.shape[3];
+  const int64_t n_kv_heads = kv.shape[2];
+  if (kv.shape[0] != batch || kv.shape[1] != seq_len || kv.shape[3] != head_dim) {
+    shape_mismatch("q and k must share batch/seq_len/head_dim; got q=" + shape_str(qv.shape) +
+                   ", k=" + shape_str(kv.shape));
+  }
+  if (head_dim % 2 != 0) shape_mismatch("head_dim must be even, got " + std::to_string(head_dim));
+  const int64_t half = head_dim / 2;
+  const std::vector<int64_t> table{seq_len, half};
+  if (cv.shape != table || sv.shape != table) {
+    shape_mismatch("cos/sin must have shape [" + std::to_string(seq_len) + ", " + std::to_string(half) +
+                   "]; got cos=" + shape_str(cv.shape) + ", sin=" + shape_str(sv.shape));
+  }
+  void* st = current_stream(qv.device_index);
+  check_launch("launch_rope_fwd",
+               launch_rope_fwd((const void*)qv.ptr, (const void*)kv.ptr, (const void*)cv.ptr,
+                               (const void*)sv.ptr, (void*)qov.ptr, (void*)kov.ptr, batch, seq_len,
+                               n_q_heads, n_kv_heads, head_dim, qv.dtype, st));
+}
+
+// Shared checks of the FP8 bindings (src/kernels/fp8_quant.rs:71-99).
+void check_fp8_common(const View& xv, const View& qv, int32_t fmt, const std::string& fmt_str) {
+  require_fp8_out(qv, fmt, fmt_str, "x_fp8");
+}
+
+void check_2d_and_codes(const View& xv, const View& qv) {
+  if (xv.shape.size() != 2) shape_mismatch("x must be 2-D [M, N]; got " + shape_str(xv.shape));
+  const int64_t m = xv.shape[0], n = xv.shape[1];
+  if (qv.shape != std::vector<int64_t>{m, n}) {
+    shape_mismatch("x_fp8 shape " + shape_str(qv.shape) + " must be [" + std::to_string(m) + ", " +
+                   std::to_string(n) + "]");
+  }
+}
+
+// src/kernels/fp8_quant.rs:61-131
+void fp8_quant_block_fwd(py::handle x, py::handle x_fp8, py::handle scale, const std::string& fmt_str) {
+  const int32_t fmt = parse_fp8_format(fmt_str);
+  View xv = validate_tensor("x", x);
+  View qv = validate_tensor("x_fp8", x_fp8);
+  View sv = validate_tensor("scale", scale);
+  check_fp8_common(xv, qv, fmt, fmt_str);
+  require_f32("scale", sv);
+  check_2d_and_codes(xv, qv);
+  const int64_t m = xv.shape[0], n = xv.shape[1];
+  const int64_t nrb = (m + 127) / 128, ncb = (n + 127) / 128;
+  if (sv.shape != std::vector<int64_t>{nrb, ncb}) {
+    shape_mismatch("scale shape " + shape_str(sv.shape) + " must be [" + std::to_string(nrb) + ", " +
+                   std::to_string(ncb) + "] (ceil(M/128), ceil(N/128))");
+  }
+  void* st = current_stream(xv.device_index);
+  check_launch("launch_fp8_quant_block_fwd",
+               launch_fp8_quant_block_fwd((const void*)xv.ptr, (uint8_t*)qv.ptr, (float*)sv.ptr, m, n,
+                                          xv.dtype, fmt, st));
+}
+
+// src/kernels/fp8_quant.rs:138-210
+void fp8_quant_tensor_fwd(py::handle x, py::handle x_fp8, py::handle scale, py::handle amax_scratch,
+                          const std::string& fmt_str) {
+  const int32_t fmt = parse_fp8_format(fmt_str);
+  View xv = validate_tensor("x", x);
+  View qv = validate_tensor("x_fp8", x_fp8);
+  View sv = validate_tensor("scale", scale);
+  View av = validate_int32_tensor("amax_scratch", amax_scratch);
+  check_fp8_common(xv, qv, fmt, fmt_str);
+  require_f32("scale", sv);
+  check_2d_and_codes(xv, qv);
+  if (product(av.shape, 0, av.shape.size()) != 1) {
+    shape_mismatch("amax_scratch must have exactly 1 element; got shape " + shape_str(av.shape));
+  }
+  const int64_t m = xv.shape[0], n = xv.shape[1];
+  void* st = current_stream(xv.device_index);
+  check_launch("launch_fp8_quant_tensor_fwd",
+               launch_fp8_quant_tensor_fwd((const void*)xv.ptr, (uint8_t*)qv.ptr, (float*)sv.ptr,
+                                           (int32_t*)av.ptr, m, n, xv.dtype, fmt, st));
+}
+
+// ---- additive functions ----------------------------------------------------
+
+void fp8_quant_token_fwd(py::handle x, py::handle x_fp8, py::handle scale, const std::string& fmt_str) {
+  const int32_t fmt = parse_fp8_format(fmt_str);
+  View xv = validate_tensor("x", x);
+  View qv = validate_tensor("x_fp8", x_fp8);
+  View sv = validate_tensor("scale", scale);
+  check_fp8_common(xv, qv, fmt, fmt_str);
+  require_f32("scale", sv);
+  check_2d_and_codes(xv, qv);
+  const int64_t m = xv.shape[0], n = xv.shape[1];
+  if (sv.shape != std::vector<int64_t>{m}) {
+    shape_mismatch("scale shape " + shape_str(sv.shape) + " must be [" + std::to_string(m) + "] (one per row)");
+  }
+  void* st = current_stream(xv.device_index);
+  check_launch("launch_fp8_quant_token_fwd",
+               launch_fp8_quant_token_fwd((const void*)xv.ptr, (uint8_t*)qv.ptr, (float*)sv.ptr, m, n,
+                                          xv.dtype, fmt, st));
+}
+
+void fp8_quant_static_fwd(py::handle x, py::handle x_fp8, double scale, const std::string& fmt_str) {
+  const int32_t fmt = parse_fp8_format(fmt_str);
+  View xv = validate_tensor("x", x);
+  View qv = validate_tensor("x_fp8", x_fp8);
+  check_fp8_common(xv, qv, fmt, fmt_str);
+  check_2d_and_codes(xv, qv);
+  const int64_t m = xv.shape[0], n = xv.shape[1];
+  void* st = current_stream(xv.device_index);
+  check_launch("launch_fp8_quant_static_fwd",
+               launch_fp8_quant_static_fwd((const void*)xv.ptr, (uint8_t*)qv.ptr, (float)scale, m, n,
+                                           xv.dtype, fmt, st));
+}
+
+// Scale argument of the fused FP8 bindings: a float32 [rows] tensor for
+// dynamic per-token scales, or (static_scale given) unused and may be None.
+float* fused_scale_arg(py::handle scale, const std::optional<double>& static_scale, int64_t rows) {
+  if (static_scale) return nullptr;
+  if (scale.is_none()) value_error("scale must be a float32 tensor of shape [rows] when static_scale is None");
+  View sv = validate_tensor("scale", scale);
+  require_f32("scale", sv);
+  if (sv.shape != std::vector<int64_t>{rows}) {
+    shape_mismatch("scale shape " + shape_str(sv.shape) + " must be [" + std::to_string(rows) + "] (one per row)");
+  }
+  return (float*)sv.ptr;
+}
+
+void rmsnorm_residual_fp8_fwd(py::handle x, py::handle residual, py::handle weight, py::handle y_fp8,
+                              py::handle scale, py::handle residual_out, double eps,
+                              const std::string& fmt_str, std::optional<double> static_scale) {
+  const int32_t fmt = parse_fp8_format(fmt_str);
+  View xv = validate_tensor("x", x);
+  View rv = validate_tensor("residual", residual);
+  View wv = validate_tensor("weight", weight);
+  View qv = validate_tensor("y_fp8", y_fp8);
+  View rov = validate_tensor("residual_out", residual_out);
+  check_dtype_matches("residual", rv, xv, "x");
+  check_dtype_matches("weight", wv, xv, "x");
+  check_dtype_matches("residual_out", rov, xv, "x");
+  require_fp8_out(qv, fmt, fmt_str, "y_fp8");
+  if (rv.shape != xv.shape || qv.shape != xv.shape || rov.shape != xv.shape) {
+    shape_mismatch("x/residual/y_fp8/residual_out must share the same shape; got x=" + shape_str(xv.shape) +
+                   ", residual=" + shape_str(rv.shape) + ", y_fp8=" + shape_str(qv.shape) +
+                   ", residual_out=" + shape_str(rov.shape));
+  }
+  if (xv.shape.empty()) shape_mismatch("x must have at least 1 dimension");
+  const int64_t cols = xv.shape.back();
+  if (wv.shape != std::vector<int64_t>{cols}) {
+    shape_mismatch("weight shape " + shape_str(wv.shape) + " must be [" + std::to_string(cols) +
+                   "] (x's last dimension)");
+  }
+  const int64_t rows = product(xv.shape, 0, xv.shape.size() - 1);
+  float* sp = fused_scale_arg(scale, static_scale, rows);
+  void* st = current_stream(xv.device_index);
+  check_launch("launch_rmsnorm_residual_fp8_fwd",
+               launch_rmsnorm_residual_fp8_fwd(
+                   (const void*)xv.ptr, (const void*)rv.ptr, (const void*)wv.ptr, (uint8_t*)qv.ptr, sp,
+                   (void*)rov.ptr, rows, cols, (float)eps, static_scale ? (float)*static_scale : 0.0f,
+                   static_scale ? CCK_SCALE_STATIC : CCK_SCALE_TOKEN, xv.dtype, fmt, st));
+}
+
+void swiglu_fp8_fwd(py::handle gate, py::handle up, py::handle y_fp8, py::handle scale,
+                    const std::string& fmt_str, std::optional<double> static_scale) {
+  const int32_t fmt = parse_fp8_format(fmt_str);
+  View gv = validate_tensor("gate", gate);
+  View uv = validate_tensor("up", up);
+  View qv = validate_tensor("y_fp8", y_fp8);
+  check_dtype_matches("up", uv, gv, "gate");
+  require_fp8_out(qv, fmt, fmt_str, "y_fp8");
+  if (uv.shape != gv.shape || qv.shape != gv.shape) {
+    shape_mismatch("gate/up/y_fp8 must share the same shape; got gate=" + shape_str(gv.shape) +
+                   ", up=" + shape_str(uv.shape) + ", y_fp8=" + shape_str(qv.shape));
+  }
+  if (gv.shape.empty()) shape_mismatch("gate must have at least 1 dimension");
+  const int64_t cols = gv.shape.back();
+  const int64_t rows = product(gv.shape, 0, gv.shape.size() - 1);
+  float* sp = fused_scale_arg(scale, static_scale, rows);
+  void* st = current_stream(gv.device_index);
+  check_launch("launch_swiglu_fp8_fwd",
+               launch_swiglu_fp8_fwd((const void*)gv.ptr, (const void*)uv.ptr, (uint8_t*)qv.ptr, sp, rows,
+                                     cols, static_scale ? (float)*static_scale : 0.0f,
+                                     static_scale ? CCK_SCALE_STATIC : CCK_SCALE_TOKEN, gv.dtype, fmt,
+                                     st));
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_native, m) {
+  m.doc() = "Validating binding over the libcustom_kernels_amd C ABI (gfx950).";
+  m.def("rmsnorm_residual_fwd", &rmsnorm_residual_fwd, py::arg("x"), py::arg("residual"), py::arg("weight"),
+        py::arg("y"), py::arg("residual_out"), py::arg("eps"));
+  m.def("swiglu_fwd", &swiglu_fwd, py::arg("gate"), py::arg("up"), py::arg("y"));
+  m.def("rope_fwd", &rope_fwd, py::arg("q"), py::arg("k"), py::arg("cos"), py::arg("sin"), py::arg("q_out"),
+        py::arg("k_out"));
+  m.def("fp8_quant_block_fwd", &fp8_quant_block_fwd, py::arg("x"), py::arg("x_fp8"), py::arg("scale"),
+        py::arg("fp8_format"));
+  m.def("fp8_quant_tensor_fwd", &fp8_quant_tensor_fwd, py::arg("x"), py::arg("x_fp8"), py::arg("scale"),
+        py::arg("amax_scratch"), py::arg("fp8_format"));
+  m.def("fp8_quant_token_fwd", &fp8_quant_token_fwd, py::arg("x"), py::arg("x_fp8"), py::arg("scale"),
+        py::arg("fp8_format"));
+  m.def("fp8_quant_static_fwd", &fp8_quant_static_fwd, py::arg("x"), py::arg("x_fp8"), py::arg("scale"),
+        py::arg("fp8_format"));
+  m.def("rmsnorm_residual_fp8_fwd", &rmsnorm_residual_fp8_fwd, py::arg("x"), py::arg("residual"),
+        py::arg("weight"), py::arg("y_fp8"), py::arg("scale"), py::arg("residual_out"), py::arg("eps"),
+        py::arg("fp8_format"), py::arg("static_scale") = py::none());
+  m.def("swiglu_fp8_fwd", &swiglu_fp8_fwd, py::arg("gate"), py::arg("up"), py::arg("y_fp8"), py::arg("scale"),
+        py::arg("fp8_format"), py::arg("static_scale") = py::none());
+}

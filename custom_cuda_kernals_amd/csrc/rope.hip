@@ -1,0 +1,147 @@
+// Half-split rotary position embedding on q [B,S,Hq,D] and k [B,S,Hkv,D] with
+// fp32 cos/sin tables [S, D/2], for gfx950. Out-of-place or in place
+// (q_out == q, k_out == k): every thread reads both halves of its pairs
+// before writing them.
+//
+// Semantics (baselines/rope.py:129-145), with every product and sum rounded
+// separately in fp32 (no fma contraction) and the result rounded once to T:
+//   out[:D/2] = T(x1*cos - x2*sin),  out[D/2:] = T(x2*cos + x1*sin)
+// so the output is bit-identical to the eager oracle given the same tables.
+//
+// Design: a 256-thread workgroup owns TOK tokens. Within a token, a thread is
+// pinned to one VEC-wide chunk of the half dimension and walks the heads
+// (q heads first, then k heads) with a stride of the number of head lanes,
+// so its cos/sin chunk is loaded once per token and reused for every head.
+// All accesses are 16 bytes; a wave covers whole 128-byte cache lines.
+#include "launch.hpp"
+
+namespace cck {
+namespace {
+
+#pragma clang fp contract(off)
+
+template <class C, int CHUNKS, int TOK>
+__global__ __launch_bounds__(256) void rope_tokens(const void* __restrict__ q, const void* __restrict__ k,
+                                                   const float* __restrict__ cos_t,
+                                                   const float* __restrict__ sin_t, void* q_out,
+                                                   void* k_out, int64_t tokens, int64_t seq_len,
+                                                   int hq, int hkv, int head_dim) {
+  constexpr int VEC = C::VEC;
+  constexpr int LANES = 256 / TOK;          // threads per token
+  constexpr int HLANES = LANES / CHUNKS;    // head lanes per token
+  const int t_local = threadIdx.x / LANES;
+  const int c = threadIdx.x % CHUNKS;
+  const int hl = (threadIdx.x % LANES) / CHUNKS;
+  const int half = head_dim / 2;
+  const int heads = hq + hkv;
+  for (int64_t tok = (int64_t)blockIdx.x * TOK + t_local; tok < tokens; tok += (int64_t)gridDim.x * TOK) {
+    const int64_t s = tok % seq_len;
+    float cs[VEC], sn[VEC];
+    const float4* cp = reinterpret_cast<const float4*>(cos_t + s * half + c * VEC);
+    const float4* sp = reinterpret_cast<const float4*>(sin_t + s * half + c * VEC);
+#pragma unroll
+    for (int i = 0; i < VEC / 4; ++i) {
+      const float4 a = cp[i], b = sp[i];
+      cs[4 * i] = a.x; cs[4 * i + 1] = a.y; cs[4 * i + 2] = a.z; cs[4 * i + 3] = a.w;
+      sn[4 * i] = b.x; sn[4 * i + 1] = b.y; sn[4 * i + 2] = b.z; sn[4 * i + 3] = b.w;
+    }
+    for (int h = hl; h < heads; h += HLANES) {
+      const bool is_q = h < hq;
+      const char* src = is_q ? static_cast<const char*>(q) : static_cast<const char*>(k);
+      char* dst = is_q ? static_cast<char*>(q_out) : static_cast<char*>(k_out);
+      const int64_t row = is_q ? tok * hq + h : tok * hkv + (h - hq);
+      const int64_t e0 = row * head_dim + c * VEC;
+      const u32x4* p1 = reinterpret_cast<const u32x4*>(src + e0 * C::kBytes);
+      const u32x4* p2 = reinterpret_cast<const u32x4*>(src + (e0 + half) * C::kBytes);
+      float x1[VEC], x2[VEC], o1[VEC], o2[VEC];
+      C::unpack(__builtin_nontemporal_load(p1), x1);
+      C::unpack(__builtin_nontemporal_load(p2), x2);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        o1[i] = x1[i] * cs[i] - x2[i] * sn[i];
+        o2[i] = x2[i] * cs[i] + x1[i] * sn[i];
+      }
+      __builtin_nontemporal_store(C::pack(o1), reinterpret_cast<u32x4*>(dst + e0 * C::kBytes));
+      __builtin_nontemporal_store(C::pack(o2), reinterpret_cast<u32x4*>(dst + (e0 + half) * C::kBytes));
+    }
+  }
+}
+
+// Any head_dim / alignment: one thread per (token, head, pair).
+template <class C>
+__global__ __launch_bounds__(256) void rope_scalar(const void* q, const void* k,
+                                                   const float* __restrict__ cos_t,
+                                                   const float* __restrict__ sin_t, void* q_out,
+                                                   void* k_out, int64_t tokens, int64_t seq_len,
+                                                   int hq, int hkv, int head_dim) {
+  const int half = head_dim / 2;
+  const int heads = hq + hkv;
+  const int64_t total = tokens * heads * half;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+    const int j = (int)(i % half);
+    const int64_t th = i / half;
+    const int h = (int)(th % heads);
+    const int64_t tok = th / heads;
+    const int64_t s = tok % seq_len;
+    const bool is_q = h < hq;
+    const void* src = is_q ? q : k;
+    void* dst = is_q ? q_out : k_out;
+    const int64_t e0 = (is_q ? tok * hq + h : tok * hkv + (h - hq)) * head_dim + j;
+    const float c = cos_t[s * half + j], sn = sin_t[s * half + j];
+    const float x1 = C::load1(src, e0), x2 = C::load1(src, e0 + half);
+    C::store1(dst, e0, x1 * c - x2 * sn);
+    C::store1(dst, e0 + half, x2 * c + x1 * sn);
+  }
+}
+
+}  // namespace
+}  // namespace cck
+
+using namespace cck;
+
+extern "C" int32_t launch_rope_fwd(const void* q, const void* k, const void* cos_table,
+                                   const void* sin_table, void* q_out, void* k_out, int64_t batch,
+                                   int64_t seq_len, int64_t n_q_heads, int64_t n_kv_heads,
+                                   int64_t head_dim, int32_t dtype, void* stream) {
+  if (batch <= 0 || seq_len <= 0 || head_dim <= 0) return (int32_t)hipSuccess;
+  if (n_q_heads < 0 || n_kv_heads < 0 || head_dim % 2 != 0) return (int32_t)hipErrorInvalidValue;
+  if (n_q_heads + n_kv_heads == 0) return (int32_t)hipSuccess;
+  if (n_q_heads + n_kv_heads > 0x7fffffff || head_dim > 0x7fffffff) return (int32_t)hipErrorInvalidValue;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t tokens = batch * seq_len;
+  const float* ct = static_cast<const float*>(cos_table);
+  const float* sn = static_cast<const float*>(sin_table);
+  const int hq = (int)n_q_heads, hkv = (int)n_kv_heads, d = (int)head_dim;
+  return with_codec(dtype, [&](auto codec) {
+    using C = decltype(codec);
+    const int half = d / 2;
+    const bool vec_ok = (half % C::VEC == 0) && host_aligned(q, 16) && host_aligned(k, 16) &&
+                        host_aligned(q_out, 16) && host_aligned(k_out, 16) &&
+                        host_aligned(ct, 16) && host_aligned(sn, 16);
+    const int chunks = vec_ok ? half / C::VEC : 0;
+    // TOK tokens per workgroup, 256/TOK threads per token, CHUNKS chunk lanes.
+#define CCK_ROPE(CH_, TOK_)                                                                  \
+  rope_tokens<C, CH_, TOK_><<<flat_grid(tokens, TOK_, 1 << 30), 256, 0, st>>>(             \
+      q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d)
+    if (chunks == 8) {
+      CCK_ROPE(8, 4);
+    } else if (chunks == 4) {
+      CCK_ROPE(4, 8);
+    } else if (chunks == 16) {
+      CCK_ROPE(16, 2);
+    } else if (chunks == 2) {
+      CCK_ROPE(2, 16);
+    } else if (chunks == 1) {
+      CCK_ROPE(1, 32);
+    } else if (chunks == 32) {
+      CCK_ROPE(32, 1);
+    } else {
+      const int64_t total = tokens * (int64_t)(hq + hkv) * half;
+      rope_scalar<C><<<flat_grid(total, 256, 1 << 20), 256, 0, st>>>(q, k, ct, sn, q_out, k_out,
+                                                                   tokens, seq_len, hq, hkv, d);
+    }
+#undef CCK_ROPE
+    return launch_status();
+  });
+}

@@ -1,0 +1,127 @@
+/*
+ * C ABI of the MI355X (gfx950) activation-path library libcustom_kernels_amd.so.
+ *
+ * Conventions (same as the reference's csrc/includes/<op>.h launchers):
+ *   - every launcher returns a hipError_t as int32_t: 0 == success;
+ *     hipErrorInvalidValue (1) for an unknown dtype / format / mode tag,
+ *     returned before any device call; otherwise the launch status;
+ *   - all tensors are caller-allocated, contiguous, row-major device
+ *     buffers; the library never allocates, frees, copies or synchronises;
+ *   - work is enqueued asynchronously on `stream` (a hipStream_t; NULL is the
+ *     null stream);
+ *   - empty work (a dimension <= 0) returns 0 without touching the device;
+ *   - unaligned pointers and sizes that are not a multiple of the 16-byte
+ *     vector width are accepted (scalar kernels handle them).
+ *
+ * The reference declares its launchers with cudaError_t / cudaStream_t; both
+ * are 32-bit-enum / pointer sized, so these declarations are ABI-compatible
+ * with its Rust `extern "C"` blocks (src/kernels/<op>.rs declare `-> i32` and
+ * `stream: *mut c_void`).
+ */
+#ifndef CUSTOM_KERNELS_AMD_H_
+#define CUSTOM_KERNELS_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Dtype tags. Replaces KernelDType (reference csrc/includes/common.cuh:28-34,
+ * src/kernels/dtype.rs:5-25); same values. */
+enum {
+  CCK_DTYPE_F32 = 0,
+  CCK_DTYPE_F16 = 1,
+  CCK_DTYPE_BF16 = 2,
+  CCK_DTYPE_F8E4M3 = 3, /* OCP e4m3fn (torch.float8_e4m3fn) */
+  CCK_DTYPE_F8E5M2 = 4  /* OCP e5m2 (torch.float8_e5m2) */
+};
+
+/* Scale modes of the fused FP8 launchers. */
+enum {
+  CCK_SCALE_TOKEN = 0, /* dynamic, one scale per row, written to scale[rows] */
+  CCK_SCALE_STATIC = 1 /* caller-given static_scale; `scale` is not used */
+};
+
+/* residual_out = x + residual; y = rmsnorm(residual_out) * weight.
+ * x, residual, y, residual_out: [rows, cols]; weight: [cols]; one dtype.
+ * Replaces reference csrc/includes/rmsnorm_residual.h:17-27. */
+int32_t launch_rmsnorm_residual_fwd(const void* x, const void* residual, const void* weight,
+                                    void* y, void* residual_out, int64_t rows, int64_t cols,
+                                    float eps, int32_t dtype, void* stream);
+
+/* y = silu(gate) * up over n elements.
+ * Replaces reference csrc/includes/swiglu.h:16-22. */
+int32_t launch_swiglu_fwd(const void* gate, const void* up, void* y, int64_t n, int32_t dtype,
+                          void* stream);
+
+/* Half-split RoPE. q: [batch, seq_len, n_q_heads, head_dim], k: [batch, seq_len,
+ * n_kv_heads, head_dim], cos/sin: float32 [seq_len, head_dim/2]. q_out may equal
+ * q and k_out may equal k (in place). head_dim must be even.
+ * Replaces reference csrc/includes/rope.h:23-36. */
+int32_t launch_rope_fwd(const void* q, const void* k, const void* cos_table, const void* sin_table,
+                        void* q_out, void* k_out, int64_t batch, int64_t seq_len,
+                        int64_t n_q_heads, int64_t n_kv_heads, int64_t head_dim, int32_t dtype,
+                        void* stream);
+
+/* Dynamic FP8, one scale per 128x128 tile; scale: float32 [ceil(m/128), ceil(n/128)].
+ * fp8_format: CCK_DTYPE_F8E4M3 or CCK_DTYPE_F8E5M2.
+ * Replaces reference csrc/includes/fp8_quant.h:41-49. */
+int32_t launch_fp8_quant_block_fwd(const void* x, uint8_t* x_fp8, float* scale, int64_t m,
+                                   int64_t n, int32_t dtype, int32_t fp8_format, void* stream);
+
+/* Dynamic FP8, one scale for the matrix; scale: float32 [1]; amax_scratch:
+ * int32 [1], caller-zeroed before every call.
+ * Replaces reference csrc/includes/fp8_quant.h:51-60. */
+int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, float* scale,
+                                    int32_t* amax_scratch, int64_t m, int64_t n, int32_t dtype,
+                                    int32_t fp8_format, void* stream);
+
+/* ---- Additive entry points (no reference counterpart; they implement the
+ * per-token / static / fused FP8 modes by composing the reference's eager
+ * formulas: baselines/fp8_quant.py:162-178 per row, baselines/rmsnorm_residual.py:123-136,
+ * baselines/swiglu.py:107-112). ---- */
+
+/* Dynamic FP8, one scale per row; scale: float32 [m]. */
+int32_t launch_fp8_quant_token_fwd(const void* x, uint8_t* x_fp8, float* scale, int64_t m,
+                                   int64_t n, int32_t dtype, int32_t fp8_format, void* stream);
+
+/* FP8 with a caller-given scale: x_fp8 = fp8(x / scale). */
+int32_t launch_fp8_quant_static_fwd(const void* x, uint8_t* x_fp8, float scale, int64_t m,
+                                    int64_t n, int32_t dtype, int32_t fp8_format, void* stream);
+
+/* residual_out = x + residual, and the FP8 codes of y = rmsnorm(residual_out) * weight
+ * (y rounded to dtype first; y itself is not written). scale_mode CCK_SCALE_TOKEN
+ * writes scale[rows]; CCK_SCALE_STATIC uses static_scale. */
+int32_t launch_rmsnorm_residual_fp8_fwd(const void* x, const void* residual, const void* weight,
+                                        uint8_t* y_fp8, float* scale, void* residual_out,
+                                        int64_t rows, int64_t cols, float eps, float static_scale,
+                                        int32_t scale_mode, int32_t dtype, int32_t fp8_format,
+                                        void* stream);
+
+/* FP8 codes of y = silu(gate) * up (y rounded to dtype first), rows of length cols.
+ * scale_mode as above. */
+int32_t launch_swiglu_fp8_fwd(const void* gate, const void* up, uint8_t* y_fp8, float* scale,
+                              int64_t rows, int64_t cols, float static_scale, int32_t scale_mode,
+                              int32_t dtype, int32_t fp8_format, void* stream);
+
+/* ---- Diagnostics (no reference counterpart): device-side checks of the
+ * arithmetic shortcuts used on the FP8 fast path. ---- */
+
+/* Compares the hardware fp32->fp8 conversion with the exact encoder for every
+ * fp32 bit pattern in [start, start + count). counters: 8 x u64, zeroed, with
+ * [4..7] preset to UINT64_MAX; see csrc/selftest.hip for the layout. */
+int32_t cck_fp8_cvt_selftest(uint64_t start, uint64_t count, int32_t fp8_format,
+                             unsigned long long* counters, void* stream);
+
+/* Compares the three-op division with IEEE x / s for every (x, s) pair inside
+ * the fast-path domain. counters: 5 x u64, zeroed, with [3] preset to
+ * UINT64_MAX; see csrc/selftest.hip for the layout. */
+int32_t cck_div_selftest(const float* xs, int64_t nx, const float* ss, int64_t ns,
+                         unsigned long long* counters, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUSTOM_KERNELS_AMD_H_ */

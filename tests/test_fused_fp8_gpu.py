@@ -1,0 +1,103 @@
+"""Fused RMSNorm+FP8 and SwiGLU+FP8 kernels.
+
+Parity definition (a fused op's codes depend on its own bf16 intermediate):
+* codes and scales are bit-exact against the oracle quantisation of the
+  kernel's own intermediate, produced by the unfused kernel of this library
+  (which is itself checked against the eager oracle within one ulp in
+  test_rmsnorm_residual_gpu.py / test_swiglu_gpu.py);
+* residual_out is bit-exact against the eager oracle;
+* the fraction of codes that also equal the strict composed-eager oracle is
+  printed (it differs only where the intermediate is one ulp apart).
+Workloads: BASELINE configs 3v and 5 (per-token and static 0.05) at full size,
+plus small and ragged shapes in all dtypes / formats.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from custom_cuda_kernals_amd.kernels import rmsnorm_residual, rmsnorm_residual_fp8, swiglu, swiglu_fp8
+from oracle import eager, inputs
+from oracle import fp8 as ofp8
+from tests._parity import assert_codes_equal, assert_f32_bits_equal, bits_equal, codes_np
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+def _quant(y: torch.Tensor, fmt, static):
+    y2 = y.float().cpu().numpy().reshape(-1, y.shape[-1])
+    if static is None:
+        return ofp8.quant_token(y2, fmt)
+    return ofp8.quant_static(y2, static, fmt), np.array([static], dtype=np.float32)
+
+
+def _check_rms(x, r, w, eps, fmt, static):
+    xd, rd, wd = x.cuda(), r.cuda(), w.cuda()
+    q, s, ro = rmsnorm_residual_fp8(xd, rd, wd, eps, fp8_format=fmt, scale=static)
+    y_k, _ = rmsnorm_residual(xd, rd, wd, eps)
+    codes, s_ref = _quant(y_k, fmt, static)
+    assert_codes_equal(q, codes.reshape(q.shape))
+    assert_f32_bits_equal(s, s_ref.reshape(s.shape) if static is None else s_ref)
+    _, ro_ref = eager.rmsnorm_residual(x, r, w, eps)
+    assert bits_equal(ro, ro_ref).all()
+    strict, _, _, _ = eager.rmsnorm_residual_fp8(x, r, w, eps, fmt, static)
+    print(f"\nrmsnorm+fp8 {tuple(x.shape)} {x.dtype} {fmt} static={static}: "
+          f"strict-eager code agreement {float((codes_np(q).reshape(strict.shape) == strict).mean()):.7f}")
+
+
+def _check_swiglu(g, u, fmt, static):
+    gd, ud = g.cuda(), u.cuda()
+    q, s = swiglu_fp8(gd, ud, fp8_format=fmt, scale=static)
+    y_k = swiglu(gd, ud)
+    codes, s_ref = _quant(y_k, fmt, static)
+    assert_codes_equal(q, codes.reshape(q.shape))
+    assert_f32_bits_equal(s, s_ref.reshape(s.shape) if static is None else s_ref)
+    strict, _, _ = eager.swiglu_fp8(g, u, fmt, static)
+    print(f"\nswiglu+fp8 {tuple(g.shape)} {g.dtype} {fmt} static={static}: "
+          f"strict-eager code agreement {float((codes_np(q).reshape(strict.shape) == strict).mean()):.7f}")
+
+
+@pytest.mark.parametrize("static", [None, 0.05])
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("shape", [(64, 4096), (17, 100), (3, 40000), (5, 11008)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_rmsnorm_fp8_small(shape, dtype, fmt, static):
+    x, r, w = inputs.rmsnorm_inputs(*shape, dtype, seed=shape[1])
+    _check_rms(x, r, w, 1e-5, fmt, static)
+
+
+@pytest.mark.parametrize("static", [None, 0.05])
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("shape", [(64, 14336), (17, 100), (3, 40000), (5, 11008)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_swiglu_fp8_small(shape, dtype, fmt, static):
+    g, u = inputs.swiglu_inputs(*shape, dtype, seed=shape[1])
+    if static is not None:
+        g = g * 3  # push some |y| / 0.05 past the e4m3 range (NaN codes)
+    _check_swiglu(g, u, fmt, static)
+
+
+def test_config3v_swiglu_fp8_full_size():
+    g, u = inputs.swiglu_inputs(*inputs.CONFIG_SHAPES["swiglu"], torch.bfloat16, seed=0)
+    _check_swiglu(g, u, "e4m3", None)
+
+
+@pytest.mark.parametrize("static", [None, inputs.STATIC_SCALE])
+def test_config5_chain_full_size(static):
+    x, r, w = inputs.rmsnorm_inputs(*inputs.CONFIG_SHAPES["chain_rmsnorm"], torch.bfloat16, seed=0)
+    _check_rms(x, r, w, inputs.RMS_EPS, "e4m3", static)
+    del x, r, w
+    g, u = inputs.swiglu_inputs(*inputs.CONFIG_SHAPES["chain_swiglu"], torch.bfloat16, seed=1)
+    _check_swiglu(g, u, "e4m3", static)
+
+
+def test_fused_rejections():
+    x = torch.randn(4, 8, device="cuda")
+    with pytest.raises(ValueError):
+        rmsnorm_residual_fp8(x, x, torch.randn(8, device="cuda"), fp8_format="e3m4")
+    with pytest.raises(ValueError):
+        swiglu_fp8(x, torch.randn(4, 8, device="cuda", dtype=torch.float16))

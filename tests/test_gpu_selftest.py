@@ -1,0 +1,78 @@
+"""Device-side checks of the two arithmetic shortcuts of the FP8 fast path,
+run through the C ABI diagnostics (csrc/selftest.hip):
+
+* gfx950's v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32 against the exact encoder
+  (itself pinned to torch's cast and to the oracle in test_oracle_fp8.py) for
+  all 2^32 fp32 bit patterns;
+* the three-op division against IEEE division for every finite bf16 x and a
+  large set of scales (random mantissas, every dynamic scale a bf16 amax can
+  produce, and edge scales).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from tests import _cck
+
+pytestmark = pytest.mark.gpu
+
+FMT_TAG = {"e4m3": 3, "e5m2": 4}
+FAST_LIMIT = {"e4m3": 448.0, "e5m2": 57344.0}
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_hw_fp8_convert_matches_exact_encoder_on_fast_domain(fmt):
+    lib = _cck.load()
+    counters = torch.zeros(8, dtype=torch.int64, device="cuda")
+    counters[4:] = -1
+    stream = torch.cuda.current_stream().cuda_stream
+    chunk = 1 << 30
+    for start in range(0, 1 << 32, chunk):
+        assert lib.cck_fp8_cvt_selftest(start, chunk, FMT_TAG[fmt], counters.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    c = counters.cpu().numpy().view(np.uint64)
+    print(f"\n[{fmt}] hw-vs-exact mismatches: |v|<={FAST_LIMIT[fmt]}: {c[0]}, above: {c[1]} "
+          f"(lowest {hex(int(c[5]))}), inf: {c[2]}, nan: {c[3]} (lowest {hex(int(c[7]))})")
+    assert c[0] == 0, f"hardware conversion differs inside the fast domain, first pattern {hex(int(c[4]))}"
+
+
+def _finite_bf16_values() -> np.ndarray:
+    v = (np.arange(1 << 16, dtype=np.uint32) << 16).view(np.float32)
+    return v[np.isfinite(v)]
+
+
+def _scales() -> np.ndarray:
+    rng = np.random.default_rng(0)
+    mant = rng.integers(0, 1 << 23, size=1 << 20, dtype=np.uint32)
+    random_scales = ((np.uint32(127) << 23) | mant).view(np.float32)  # [1, 2)
+    amax = _finite_bf16_values()
+    amax = np.abs(amax[amax > 0])
+    dyn = []
+    for fmax in (448.0, 57344.0):
+        s = amax / np.float32(fmax)
+        dyn.append(np.where(s < np.float32(1e-12), np.float32(1e-12), s).astype(np.float32))
+    edge = np.array([1e-12, 0.05, 1.0, 3.0, 7.0, 1.1754944e-38, 2.0**-100, 2.0**100, 1e30], dtype=np.float32)
+    return np.unique(np.concatenate([random_scales, *dyn, edge]).astype(np.float32))
+
+
+def test_fast_division_matches_ieee_division():
+    lib = _cck.load()
+    xs = torch.from_numpy(_finite_bf16_values()).cuda()
+    ss = torch.from_numpy(_scales()).cuda()
+    counters = torch.zeros(5, dtype=torch.int64, device="cuda")
+    counters[3] = -1
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.cck_div_selftest(xs.data_ptr(), xs.numel(), ss.data_ptr(), ss.numel(), counters.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    c = counters.cpu().numpy().view(np.uint64)
+    print(f"\npairs checked {c[4]}, fp32 bit mismatches {c[0]}, e4m3 code mismatches {c[1]}, "
+          f"e5m2 code mismatches {c[2]}")
+    if c[0]:
+        i = int(c[3])
+        x, s = xs[i % xs.numel()].item(), ss[i // xs.numel()].item()
+        print(f"first bitwise mismatch: x={x!r} s={s!r}")
+    assert c[4] > 10**10
+    assert c[1] == 0 and c[2] == 0

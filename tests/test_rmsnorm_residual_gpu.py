@@ -1,0 +1,77 @@
+"""Fused residual + RMSNorm kernel vs the CPU oracle (torch-CPU restatement of
+baselines/rmsnorm_residual.py:123-136).
+
+* residual_out: bit-exact (one rounding of x + residual);
+* y: within one ulp of the storage type relative (bf16 2^-7, fp16 2^-10) and
+  1e-5 relative in fp32; the fraction of bit-identical elements is printed.
+Shapes: the reference's standard + edge cases (baselines/rmsnorm_residual.py:75-91)
+and the BASELINE config-2 workload at full size.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from custom_cuda_kernals_amd.kernels import rmsnorm_residual
+from oracle import eager, inputs
+from tests._parity import assert_within_rel, bits_equal
+
+pytestmark = pytest.mark.gpu
+
+REL = {torch.float32: 1e-5, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
+OUTLIERS = 1e-6
+CASES = [(4, 128, 768), (2, 2048, 4096), (1, 4096, 4096), (3, 17, 4096), (2, 64, 100), (8, 1, 4096),
+         (1, 8192, 2048), (0, 128, 4096), (1, 1, 128)]
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+def _run(x, r, w, eps, x_dev=None, r_dev=None):
+    y, ro = rmsnorm_residual(x.cuda() if x_dev is None else x_dev, r.cuda() if r_dev is None else r_dev,
+                             w.cuda(), eps)
+    y_ref, ro_ref = eager.rmsnorm_residual(x, r, w, eps)
+    assert y.shape == x.shape and ro.shape == x.shape and y.dtype == x.dtype and ro.dtype == x.dtype
+    if x.numel() == 0:
+        return None
+    assert bits_equal(ro, ro_ref).all(), "residual_out must be bit-exact"
+    stats = assert_within_rel(y, y_ref, REL[x.dtype], "y", max_outlier_fraction=OUTLIERS)
+    print(f"\n{tuple(x.shape)} {x.dtype}: {stats}")
+    return stats
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c)))
+def test_matches_oracle(case, dtype):
+    b, s, h = case
+    x, r, w = inputs.rmsnorm_inputs(b * s, h, dtype, seed=b + s + h)
+    _run(x.view(b, s, h), r.view(b, s, h), w, 1e-6)
+
+
+def test_config2_full_size():
+    rows, cols = inputs.CONFIG_SHAPES["rmsnorm"]
+    x, r, w = inputs.rmsnorm_inputs(rows, cols, torch.bfloat16, seed=0)
+    stats = _run(x, r, w, inputs.RMS_EPS)
+    assert stats["bit_exact_fraction"] > 0.999
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_unaligned_and_long_rows(dtype):
+    rows, cols = 6, 40000
+    x, r, w = inputs.rmsnorm_inputs(rows, cols, dtype, seed=1)
+    _run(x, r, w, 1e-5)
+    # unaligned base pointers take the scalar path
+    xb = torch.cat([torch.zeros(1, dtype=dtype), x[:3, :1000].reshape(-1)])
+    rb = torch.cat([torch.zeros(1, dtype=dtype), r[:3, :1000].reshape(-1)])
+    xd, rd = xb.cuda()[1:].view(3, 1000), rb.cuda()[1:].view(3, 1000)
+    assert xd.data_ptr() % 16 != 0
+    _run(x[:3, :1000].contiguous(), r[:3, :1000].contiguous(), w[:1000].contiguous(), 1e-5, xd, rd)
+
+
+def test_rejections():
+    x = torch.randn(2, 4, 8, device="cuda")
+    with pytest.raises(ValueError):
+        rmsnorm_residual(x, torch.randn(2, 4, 8, device="cuda", dtype=torch.float16), torch.randn(8, device="cuda"))
+    with pytest.raises(ValueError):
+        rmsnorm_residual(x, torch.randn(2, 4, 16, device="cuda")[..., ::2], torch.randn(8, device="cuda"))
+    with pytest.raises(ValueError):
+        rmsnorm_residual(x, x, torch.randn(9, device="cuda"))

@@ -1,0 +1,67 @@
+"""SwiGLU kernel vs the CPU oracle (torch-CPU restatement of
+baselines/swiglu.py:107-112): within one storage-type ulp relative (bf16
+2^-7, fp16 2^-10), 1e-5 relative in fp32. Shapes: the reference's case table
+(baselines/swiglu.py:70-88), the vector-tail sizes n = 1..129 its kernel
+tests sweep (tests/test_swiglu_kernel.py:74-93), BASELINE config 3 at full size.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from custom_cuda_kernals_amd.kernels import swiglu
+from oracle import eager, inputs
+from tests._parity import assert_within_rel
+
+pytestmark = pytest.mark.gpu
+
+REL = {torch.float32: 1e-5, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
+OUTLIERS = 1e-6
+CASES = [(4, 128, 3072), (2, 2048, 11008), (1, 4096, 11008), (3, 17, 11008), (2, 64, 100), (8, 1, 11008),
+         (1, 8192, 4096), (0, 128, 11008), (1, 1, 128)]
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+def _run(g, u):
+    y = swiglu(g.cuda(), u.cuda())
+    y_ref = eager.swiglu(g, u)
+    assert y.shape == g.shape and y.dtype == g.dtype
+    if g.numel() == 0:
+        return None
+    stats = assert_within_rel(y, y_ref, REL[g.dtype], "y", max_outlier_fraction=OUTLIERS)
+    print(f"\n{tuple(g.shape)} {g.dtype}: {stats}")
+    return stats
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c)))
+def test_matches_oracle(case, dtype):
+    b, s, d = case
+    g, u = inputs.swiglu_inputs(b * s, d, dtype, seed=b + s + d)
+    _run(g.view(b, s, d), u.view(b, s, d))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_vector_tail_sizes(dtype):
+    for n in range(1, 130):
+        g, u = inputs.swiglu_inputs(1, n, dtype, seed=n)
+        _run(g.view(-1), u.view(-1))
+
+
+def test_config3_full_size():
+    rows, cols = inputs.CONFIG_SHAPES["swiglu"]
+    g, u = inputs.swiglu_inputs(rows, cols, torch.bfloat16, seed=0)
+    stats = _run(g, u)
+    assert stats["bit_exact_fraction"] > 0.999
+
+
+def test_extreme_gate_values():
+    g = torch.tensor([0.0, -0.0, 1e-30, -1e-30, 30.0, -30.0, 88.0, -88.0, 100.0, -100.0, -1000.0, 1000.0,
+                      float("inf"), float("-inf")], dtype=torch.float32)
+    u = torch.full_like(g, 1.5)
+    y = swiglu(g.cuda(), u.cuda()).cpu()
+    y_ref = eager.swiglu(g, u)
+    assert torch.equal(torch.isnan(y), torch.isnan(y_ref))
+    fin = ~torch.isnan(y_ref)
+    assert_within_rel(y[fin], y_ref[fin], 1e-5, "extreme")
