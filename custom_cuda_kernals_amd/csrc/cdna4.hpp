@@ -68,6 +68,7 @@ struct CodecF32 {
   }
   // Round-trip through storage precision (identity for fp32).
   __device__ static float round(float v) { return v; }
+  __device__ static void round2(float& a, float& b) {}
   __device__ static float load1(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
   __device__ static void store1(void* p, int64_t i, float v) { static_cast<float*>(p)[i] = v; }
   // |x| as order-preserving bits (NaN > inf > finite), accumulated with max.
@@ -98,6 +99,12 @@ struct CodecBF16 {
                    pack2_bf16(f[6], f[7])};
   }
   __device__ static float round(float v) { return bits_f32(pack2_bf16(v, 0.0f) << 16); }
+  // Round two values to bf16 with one v_cvt_pk_bf16_f32 (RNE) and widen back.
+  __device__ static void round2(float& a, float& b) {
+    const uint32_t w = pack2_bf16(a, b);
+    a = bf16_lo(w);
+    b = bf16_hi(w);
+  }
   __device__ static float load1(const void* p, int64_t i) {
     return bits_f32((uint32_t) static_cast<const uint16_t*>(p)[i] << 16);
   }
@@ -134,6 +141,11 @@ struct CodecF16 {
                    pack2_f16(f[6], f[7])};
   }
   __device__ static float round(float v) { return (float)(_Float16)v; }
+  __device__ static void round2(float& a, float& b) {
+    const uint32_t w = pack2_f16(a, b);
+    a = f16_lo(w);
+    b = f16_hi(w);
+  }
   __device__ static float load1(const void* p, int64_t i) {
     return (float)static_cast<const _Float16*>(p)[i];
   }
@@ -168,6 +180,16 @@ struct MaxU32 {
 struct MaxPkU16 {
   __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return pk_max_u16(a, b); }
 };
+// IEEE-754-2019 maximum on float bits: NaN-propagating (v_maximum3_f32).
+struct MaxF32 {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
+    return f32_bits(__builtin_elementwise_maximum(bits_f32(a), bits_f32(b)));
+  }
+};
+// acc = maximum(acc, |a|, |b|), NaN-propagating.
+__device__ inline float absmax2(float acc, float a, float b) {
+  return __builtin_elementwise_maximum(acc, __builtin_elementwise_maximum(__builtin_fabsf(a), __builtin_fabsf(b)));
+}
 struct AddF32 {
   __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
     return f32_bits(bits_f32(a) + bits_f32(b));
@@ -251,8 +273,13 @@ struct Fp8;
 template <>
 struct Fp8<kF8E4M3> {
   static constexpr float kMax = 448.0f;  // torch.finfo(torch.float8_e4m3fn).max
-  // Quotients with |q| <= kFastLimit are converted by v_cvt_pk_fp8_f32.
-  static constexpr float kFastLimit = 448.0f;
+  // Rows / tiles whose quotients satisfy |x| * (1/s) <= kFastLimit use the
+  // three-op division and v_cvt_pk_fp8_f32. Both were checked exhaustively on
+  // gfx950 over this range (the conversion for every finite fp32, including
+  // the NaN-for-overflow rounding above 464; the division for every finite
+  // bf16 x against a large scale set), so it spans the dynamic-scale case
+  // (|q| <= 448 * (1 + 2^-23)) with margin.
+  static constexpr float kFastLimit = 65536.0f;
   __device__ static uint32_t cvt4(float a, float b, float c, float d) {
     int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
@@ -263,7 +290,7 @@ struct Fp8<kF8E4M3> {
 template <>
 struct Fp8<kF8E5M2> {
   static constexpr float kMax = 57344.0f;  // torch.finfo(torch.float8_e5m2).max
-  static constexpr float kFastLimit = 57344.0f;
+  static constexpr float kFastLimit = 65536.0f;  // as above (infinity above 61440)
   __device__ static uint32_t cvt4(float a, float b, float c, float d) {
     int w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
     return (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true);
@@ -312,5 +339,30 @@ __device__ inline void quant_exact(const float (&v)[N], float s, uint32_t (&out)
 }
 
 __device__ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Streaming global accesses (data touched once per launch). Nontemporal by
+// default; CCK_STREAM_NT_LOAD / CCK_STREAM_NT_STORE = 0 select cached accesses.
+#ifndef CCK_STREAM_NT_LOAD
+#define CCK_STREAM_NT_LOAD 1
+#endif
+#ifndef CCK_STREAM_NT_STORE
+#define CCK_STREAM_NT_STORE 1
+#endif
+template <class T>
+__device__ inline T ld_stream(const T* p) {
+  if constexpr (CCK_STREAM_NT_LOAD) {
+    return __builtin_nontemporal_load(p);
+  } else {
+    return *p;
+  }
+}
+template <class T>
+__device__ inline void st_stream(T v, T* p) {
+  if constexpr (CCK_STREAM_NT_STORE) {
+    __builtin_nontemporal_store(v, p);
+  } else {
+    *p = v;
+  }
+}
 
 }  // namespace cck

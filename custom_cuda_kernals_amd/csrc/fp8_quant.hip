@@ -85,7 +85,7 @@ __global__ __launch_bounds__(THREADS) void fp8_token_resident(const void* __rest
     for (int k = 0; k < ITEMS; ++k) {
       const int v = threadIdx.x + k * THREADS;
       if (v < nvec) {
-        raw[k] = __builtin_nontemporal_load(xr + v);
+        raw[k] = ld_stream(xr + v);
         acc = C::absmax_vec(raw[k], acc);
       }
     }
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256) void fp8_block_resident(const void* __restrict
   for (int k = 0; k < ITEMS; ++k) {
     const int64_t row = row0 + k * RPP;
     if (col_ok && row < m) {
-      raw[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+      raw[k] = ld_stream(reinterpret_cast<const u32x4*>(
           static_cast<const char*>(x) + (row * n + col) * C::kBytes));
       acc = C::absmax_vec(raw[k], acc);
     }
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256) void fp8_tensor_amax(const void* __restrict__ 
   if constexpr (VECTOR) {
     const int64_t nvec = total / C::VEC;
     const u32x4* xv = static_cast<const u32x4*>(x);
-    for (int64_t v = tid; v < nvec; v += stride) acc = C::absmax_vec(__builtin_nontemporal_load(xv + v), acc);
+    for (int64_t v = tid; v < nvec; v += stride) acc = C::absmax_vec(ld_stream(xv + v), acc);
     for (int64_t i = nvec * C::VEC + tid; i < total; i += stride) acc = C::absmax1(x, i, acc);
   } else {
     for (int64_t i = tid; i < total; i += stride) acc = C::absmax1(x, i, acc);
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(256) void fp8_tensor_cast(const void* __restrict__ 
     const int64_t nvec = total / C::VEC;
     const u32x4* xv = static_cast<const u32x4*>(x);
     for (int64_t v = tid; v < nvec; v += stride) {
-      const u32x4 raw = __builtin_nontemporal_load(xv + v);
+      const u32x4 raw = ld_stream(xv + v);
       bool fast = fast_t;
       if constexpr (STATIC) fast = fast_path_ok<FMT>(s, r, C::absmax_to_float(C::absmax_vec(raw, 0)));
       quant_vec<C, FMT>(raw, s, r, fast, q, v * C::VEC);
@@ -271,21 +271,14 @@ int32_t launch_token(const void* x, uint8_t* q, float* scale, int64_t m, int64_t
   const bool vec_ok = (n % C::VEC == 0) && host_aligned(x, 16) && host_aligned(q, C::VEC);
   const int64_t nvec = n / C::VEC;
   const unsigned g = row_grid(m);
-  if (vec_ok && nvec <= 64) {
-    fp8_token_resident<C, FMT, 64, 1><<<g, 64, 0, st>>>(x, q, scale, m, n);
-  } else if (vec_ok && nvec <= 256) {
-    fp8_token_resident<C, FMT, 256, 1><<<g, 256, 0, st>>>(x, q, scale, m, n);
-  } else if (vec_ok && nvec <= 512) {
-    fp8_token_resident<C, FMT, 256, 2><<<g, 256, 0, st>>>(x, q, scale, m, n);
-  } else if (vec_ok && nvec <= 1024) {
-    fp8_token_resident<C, FMT, 256, 4><<<g, 256, 0, st>>>(x, q, scale, m, n);
-  } else if (vec_ok && nvec <= 2048) {
-    fp8_token_resident<C, FMT, 256, 8><<<g, 256, 0, st>>>(x, q, scale, m, n);
-  } else if (vec_ok && nvec <= 4096) {
-    fp8_token_resident<C, FMT, 512, 8><<<g, 512, 0, st>>>(x, q, scale, m, n);
-  } else {
-    fp8_token_generic<C, FMT><<<g, 256, 0, st>>>(x, q, scale, m, n);
-  }
+  auto run = [&](auto shape) {
+    using S = decltype(shape);
+    fp8_token_resident<C, FMT, S::kThreads, S::kItems><<<g, S::kThreads, 0, st>>>(x, q, scale, m, n);
+  };
+  const bool done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
+                                             RowShape<512, 2>, RowShape<1024, 2>, RowShape<1024, 4>,
+                                             RowShape<1024, 8>>(nvec, run);
+  if (!done) fp8_token_generic<C, FMT><<<g, 256, 0, st>>>(x, q, scale, m, n);
   return launch_status();
 }
 

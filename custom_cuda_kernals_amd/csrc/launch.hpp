@@ -35,6 +35,29 @@ inline int32_t with_fp8(int32_t fmt, Fn&& fn) {
   }
 }
 
+// Workgroup shape of a register-resident row kernel: THREADS threads, each
+// holding up to ITEMS 16-byte vectors of the row.
+template <int T, int I>
+struct RowShape {
+  static constexpr int kThreads = T;
+  static constexpr int kItems = I;
+};
+
+// Calls fn(S{}) for the first shape S that holds a row of nvec vectors;
+// returns false when none does (the caller then uses its looping kernel).
+template <class S, class... Rest, class Fn>
+inline bool pick_row_shape(int64_t nvec, Fn&& fn) {
+  if (nvec <= (int64_t)S::kThreads * S::kItems) {
+    fn(S{});
+    return true;
+  }
+  if constexpr (sizeof...(Rest) > 0) {
+    return pick_row_shape<Rest...>(nvec, fn);
+  } else {
+    return false;
+  }
+}
+
 inline int32_t launch_status() { return (int32_t)hipGetLastError(); }
 
 inline bool host_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
@@ -44,6 +67,19 @@ inline bool host_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a)
 inline unsigned row_grid(int64_t rows) {
   const int64_t cap = 1 << 30;
   return (unsigned)(rows < cap ? rows : cap);
+}
+
+// Compute units of the current device (cached per device ordinal).
+inline int cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
 }
 
 inline unsigned flat_grid(int64_t work_items, int threads, int64_t cap) {

@@ -22,18 +22,23 @@ namespace {
 
 #pragma clang fp contract(off)
 
+// f[i] <- T(f[i] * inv) * w[i]  (the product is rounded by the caller's store).
 template <class C>
-struct AmaxOp2 {
-  using type = MaxPkU16;
-};
-template <>
-struct AmaxOp2<CodecF32> {
-  using type = MaxU32;
-};
+__device__ inline void scale_round_mul(float (&f)[C::VEC], float inv, const float (&w)[C::VEC]) {
+#pragma unroll
+  for (int i = 0; i < C::VEC; ++i) f[i] = f[i] * inv;
+#pragma unroll
+  for (int i = 0; i < C::VEC; i += 2) C::round2(f[i], f[i + 1]);
+#pragma unroll
+  for (int i = 0; i < C::VEC; ++i) f[i] = f[i] * w[i];
+}
 
 // MODE: 0 = write y in T; 1 = FP8 codes with a per-row dynamic scale;
 // 2 = FP8 codes with a static scale.
-template <class C, int THREADS, int ITEMS, int MODE, int FMT>
+// PF: the workgroup walks rows with a stride of gridDim.x and issues the next
+// row's loads before it reduces the current one, so HBM reads overlap the
+// reduction barrier and the second (normalise / store) phase.
+template <class C, int THREADS, int ITEMS, int MODE, int FMT, bool PF>
 __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
     const void* __restrict__ x, const void* __restrict__ res, const void* __restrict__ w,
     void* __restrict__ y, uint8_t* __restrict__ yq, float* __restrict__ scale,
@@ -43,12 +48,50 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
   __shared__ uint32_t lds[2 * NW];
   const int nvec = (int)(cols / VEC);
   const u32x4* wv = static_cast<const u32x4*>(w);
-  int parity = 0;
-  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+  auto load_row = [&](int64_t row, u32x4 (&xa)[ITEMS], u32x4 (&ra)[ITEMS]) {
     const int64_t off = row * cols * C::kBytes;
     const u32x4* xr = reinterpret_cast<const u32x4*>(static_cast<const char*>(x) + off);
     const u32x4* rr = reinterpret_cast<const u32x4*>(static_cast<const char*>(res) + off);
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+      const int v = threadIdx.x + k * THREADS;
+      if (v < nvec) {
+        xa[k] = ld_stream(xr + v);
+        ra[k] = ld_stream(rr + v);
+      }
+    }
+  };
+  // The weight row is the same for every row: with few vectors per thread,
+  // load this thread's slice once, ahead of the first row; otherwise re-read
+  // it from L2 in the normalise phase (keeps wide rows within the VGPR budget).
+  constexpr bool kHoistW = ITEMS <= 2;
+  u32x4 wreg[kHoistW ? ITEMS : 1];
+  if constexpr (kHoistW) {
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+      const int v = threadIdx.x + k * THREADS;
+      if (v < nvec) wreg[k] = wv[v];
+    }
+  }
+  int parity = 0;
+  u32x4 xn[ITEMS], rn[ITEMS];
+  if constexpr (PF) {
+    if ((int64_t)blockIdx.x < rows) load_row(blockIdx.x, xn, rn);
+  }
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const int64_t off = row * cols * C::kBytes;
     u32x4* ror = reinterpret_cast<u32x4*>(static_cast<char*>(ro) + off);
+    u32x4 xa[ITEMS], ra[ITEMS];
+    if constexpr (PF) {
+#pragma unroll
+      for (int k = 0; k < ITEMS; ++k) {
+        xa[k] = xn[k];
+        ra[k] = rn[k];
+      }
+      if (row + gridDim.x < rows) load_row(row + gridDim.x, xn, rn);
+    } else {
+      load_row(row, xa, ra);
+    }
     u32x4 rov[ITEMS];
     float acc = 0.0f;
 #pragma unroll
@@ -56,12 +99,12 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
       const int v = threadIdx.x + k * THREADS;
       if (v < nvec) {
         float fx[VEC], fr[VEC], fo[VEC];
-        C::unpack(__builtin_nontemporal_load(xr + v), fx);
-        C::unpack(__builtin_nontemporal_load(rr + v), fr);
+        C::unpack(xa[k], fx);
+        C::unpack(ra[k], fr);
 #pragma unroll
         for (int i = 0; i < VEC; ++i) fo[i] = fx[i] + fr[i];
         rov[k] = C::pack(fo);
-        __builtin_nontemporal_store(rov[k], ror + v);
+        st_stream(rov[k], ror + v);
         C::unpack(rov[k], fo);
 #pragma unroll
         for (int i = 0; i < VEC; ++i) acc += fo[i] * fo[i];
@@ -80,41 +123,38 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
         if (v < nvec) {
           float fo[VEC], fw[VEC];
           C::unpack(rov[k], fo);
-          C::unpack(wv[v], fw);
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) fo[i] = C::round(fo[i] * inv) * fw[i];
-          __builtin_nontemporal_store(C::pack(fo), yr + v);
+          C::unpack(kHoistW ? wreg[kHoistW ? k : 0] : wv[v], fw);
+          scale_round_mul<C>(fo, inv, fw);
+          st_stream(C::pack(fo), yr + v);
         }
       }
     } else {
-      // y rounded to T, kept packed; amax over |y| for the dynamic scale.
-      uint32_t amax_acc = 0;
+      // y rounded to T and kept as floats; NaN-propagating amax over |y|.
+      float yv[ITEMS][VEC];
+      float amax = 0.0f;
 #pragma unroll
       for (int k = 0; k < ITEMS; ++k) {
         const int v = threadIdx.x + k * THREADS;
         if (v < nvec) {
-          float fo[VEC], fw[VEC];
-          C::unpack(rov[k], fo);
-          C::unpack(wv[v], fw);
+          float fw[VEC];
+          C::unpack(rov[k], yv[k]);
+          C::unpack(kHoistW ? wreg[kHoistW ? k : 0] : wv[v], fw);
+          scale_round_mul<C>(yv[k], inv, fw);
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) fo[i] = C::round(fo[i] * inv) * fw[i];
-          rov[k] = C::pack(fo);
-          amax_acc = C::absmax_vec(rov[k], amax_acc);
+          for (int i = 0; i < VEC; i += 2) {
+            C::round2(yv[k][i], yv[k][i + 1]);
+            amax = absmax2(amax, yv[k][i], yv[k][i + 1]);
+          }
         }
       }
-      float s, amax;
+      amax = bits_f32(block_allreduce<NW>(f32_bits(amax), MaxF32{}, lds, parity));
+      parity ^= 1;
+      float s;
       if constexpr (MODE == 1) {
-        amax_acc = block_allreduce<NW>(amax_acc, typename AmaxOp2<C>::type{}, lds, parity);
-        parity ^= 1;
-        amax = C::absmax_to_float(amax_acc);
         s = scale_from_amax<FMT>(amax);
         if (threadIdx.x == 0) scale[row] = s;
       } else {
-        // Static scale: the fast/exact choice only needs this row's amax.
-        amax_acc = block_allreduce<NW>(amax_acc, typename AmaxOp2<C>::type{}, lds, parity);
-        parity ^= 1;
-        amax = C::absmax_to_float(amax_acc);
-        s = static_scale;
+        s = static_scale;  // the row amax only selects the fast or exact path
       }
       const float r = 1.0f / s;
       const bool fast = fast_path_ok<FMT>(s, r, amax);
@@ -123,18 +163,16 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
       for (int k = 0; k < ITEMS; ++k) {
         const int v = threadIdx.x + k * THREADS;
         if (v < nvec) {
-          float fy[VEC];
-          C::unpack(rov[k], fy);
           uint32_t wq[VEC / 4];
           if (fast) {
-            quant_fast<FMT, VEC>(fy, s, r, wq);
+            quant_fast<FMT, VEC>(yv[k], s, r, wq);
           } else {
-            quant_exact<FMT, VEC>(fy, s, wq);
+            quant_exact<FMT, VEC>(yv[k], s, wq);
           }
           if constexpr (VEC == 8) {
-            __builtin_nontemporal_store((u32x2){wq[0], wq[1]}, reinterpret_cast<u32x2*>(qr + (int64_t)v * 8));
+            st_stream((u32x2){wq[0], wq[1]}, reinterpret_cast<u32x2*>(qr + (int64_t)v * 8));
           } else {
-            __builtin_nontemporal_store(wq[0], reinterpret_cast<uint32_t*>(qr + (int64_t)v * 4));
+            st_stream(wq[0], reinterpret_cast<uint32_t*>(qr + (int64_t)v * 4));
           }
         }
       }
@@ -202,24 +240,26 @@ int32_t launch_rmsnorm(const void* x, const void* res, const void* w, void* y, u
                       (MODE == 0 ? host_aligned(y, 16) : host_aligned(yq, C::VEC));
   const int64_t nvec = cols / C::VEC;
   const unsigned g = row_grid(rows);
-#define CCK_RMS(T_, I_) \
-  rmsnorm_resident<C, T_, I_, MODE, FMT><<<g, T_, 0, st>>>(x, res, w, y, yq, scale, ro, rows, cols, eps, static_scale)
-  if (vec_ok && nvec <= 64) {
-    CCK_RMS(64, 1);
-  } else if (vec_ok && nvec <= 256) {
-    CCK_RMS(256, 1);
-  } else if (vec_ok && nvec <= 512) {
-    CCK_RMS(256, 2);
-  } else if (vec_ok && nvec <= 1024) {
-    CCK_RMS(256, 4);
-  } else if (vec_ok && nvec <= 2048) {
-    CCK_RMS(256, 8);
-  } else if (vec_ok && nvec <= 4096) {
-    CCK_RMS(512, 8);
+  auto run = [&](auto shape) {
+    using S = decltype(shape);
+    rmsnorm_resident<C, S::kThreads, S::kItems, MODE, FMT, false><<<g, S::kThreads, 0, st>>>(
+        x, res, w, y, yq, scale, ro, rows, cols, eps, static_scale);
+  };
+  // Shapes measured on MI355X at cols = 4096 bf16: one vector per thread is
+  // fastest for the plain op, two per thread for the FP8 variants.
+  bool done;
+  if constexpr (MODE == 0) {
+    done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<512, 1>,
+                                    RowShape<1024, 1>, RowShape<1024, 2>,
+                                    RowShape<1024, 4>>(nvec, run);
   } else {
+    done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
+                                    RowShape<512, 2>, RowShape<1024, 2>,
+                                    RowShape<1024, 4>>(nvec, run);
+  }
+  if (!done) {
     rmsnorm_generic<C, MODE, FMT><<<g, 256, 0, st>>>(x, res, w, y, yq, scale, ro, rows, cols, eps, static_scale);
   }
-#undef CCK_RMS
   return launch_status();
 }
 

@@ -54,15 +54,15 @@ __global__ __launch_bounds__(256) void rope_tokens(const void* __restrict__ q, c
       const u32x4* p1 = reinterpret_cast<const u32x4*>(src + e0 * C::kBytes);
       const u32x4* p2 = reinterpret_cast<const u32x4*>(src + (e0 + half) * C::kBytes);
       float x1[VEC], x2[VEC], o1[VEC], o2[VEC];
-      C::unpack(__builtin_nontemporal_load(p1), x1);
-      C::unpack(__builtin_nontemporal_load(p2), x2);
+      C::unpack(ld_stream(p1), x1);
+      C::unpack(ld_stream(p2), x2);
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
         o1[i] = x1[i] * cs[i] - x2[i] * sn[i];
         o2[i] = x2[i] * cs[i] + x1[i] * sn[i];
       }
-      __builtin_nontemporal_store(C::pack(o1), reinterpret_cast<u32x4*>(dst + e0 * C::kBytes));
-      __builtin_nontemporal_store(C::pack(o2), reinterpret_cast<u32x4*>(dst + (e0 + half) * C::kBytes));
+      st_stream(C::pack(o1), reinterpret_cast<u32x4*>(dst + e0 * C::kBytes));
+      st_stream(C::pack(o2), reinterpret_cast<u32x4*>(dst + (e0 + half) * C::kBytes));
     }
   }
 }
@@ -125,7 +125,7 @@ extern "C" int32_t launch_rope_fwd(const void* q, const void* k, const void* cos
   rope_tokens<C, CH_, TOK_><<<flat_grid(tokens, TOK_, 1 << 30), 256, 0, st>>>(             \
       q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d)
     if (chunks == 8) {
-      CCK_ROPE(8, 4);
+      CCK_ROPE(8, 1);  // measured fastest on MI355X for head_dim 128 bf16
     } else if (chunks == 4) {
       CCK_ROPE(4, 8);
     } else if (chunks == 16) {

@@ -9,10 +9,17 @@
 // (dynamic, per token) or with a static scale and does not write y itself.
 //
 // Design: the plain op is a flat grid-stride stream of 16-byte vectors (two
-// loads, one store per vector, nontemporal so the 1.4 GB stream does not
-// evict anything useful). The FP8 variant is row-resident: one workgroup per
-// row keeps y packed in registers while it reduces the row amax, so gate/up
-// are read once and only the codes and the scale are written.
+// loads, one store per vector). The FP8 variant is row-resident: one
+// workgroup per row keeps y in registers while it reduces the row amax, so
+// gate/up are read once and only the codes and the scale are written.
+//
+// The op is close to VALU-bound on gfx950 (no packed fp32 here), so sigmoid is
+// built for instruction count: exp(-g) = 2^th * (1 + c) with one v_exp_f32,
+// and 1/(1+e) = one v_rcp_f32 plus a Newton step. For bf16 inputs, th = -g*HI
+// is exact (8-bit g times a 16-bit HI), so only the tiny c = -g*LO*ln2 is
+// rounded; other input types split the product with an fma. Vectors with a
+// gate below the fast range (exp(-g) near overflow, sigmoid subnormal) use the
+// IEEE expf / division path.
 #include "launch.hpp"
 
 namespace cck {
@@ -20,15 +27,69 @@ namespace {
 
 #pragma clang fp contract(off)
 
-// sigmoid(g) = 1 / (1 + exp(-g)): exp to ~1 ulp (ocml), reciprocal refined by
-// one Newton step with a fused remainder, i.e. within an ulp of the
-// correctly rounded 1/d.
-__device__ inline float silu(float g) {
-  const float d = 1.0f + __builtin_expf(-g);
+// log2(e) = HI + LO; HI has 16 significant bits so g * HI is exact for bf16 g.
+template <class C>
+struct SiluConsts {
+  static constexpr bool kExactHi = false;
+  static constexpr float kHi = 1.44269502162933349609375f;  // RN32(log2 e)
+  static constexpr float kLo = 1.925963033500011e-08f;       // log2 e - kHi
+  static constexpr float kFastMin = -87.0f;                  // sigmoid stays normal
+};
+template <>
+struct SiluConsts<CodecBF16> {
+  static constexpr bool kExactHi = true;
+  static constexpr float kHi = 1.44268798828125f;
+  static constexpr float kLoLn2 = 4.888495368504664e-06f;  // (log2 e - kHi) * ln 2
+  // First-order correction 1 + c is within an ulp for |c| < 1e-4 (|g| < 20).
+  static constexpr float kFastMin = -20.0f;
+};
+
+constexpr float kLn2 = 0.693147182464599609375f;
+
+template <class C>
+__device__ inline float exp_neg_fast(float g) {
+  using K = SiluConsts<C>;
+  if constexpr (K::kExactHi) {
+    const float th = g * -K::kHi;  // exact
+    const float c = g * -K::kLoLn2;
+    const float p = __builtin_amdgcn_exp2f(th);
+    return __builtin_fmaf(p, c, p);
+  } else {
+    const float th = g * -K::kHi;
+    const float rem = __builtin_fmaf(g, -K::kHi, -th);  // exact remainder of the product
+    const float tl = __builtin_fmaf(g, -K::kLo, rem);
+    const float p = __builtin_amdgcn_exp2f(th);
+    return __builtin_fmaf(p, tl * kLn2, p);
+  }
+}
+
+// 1 / d to within an ulp: v_rcp_f32 then one Newton step with a fused remainder.
+__device__ inline float recip_refined(float d) {
   const float r0 = __builtin_amdgcn_rcpf(d);
   const float e = __builtin_fmaf(-d, r0, 1.0f);
-  const float sig = __builtin_fmaf(e, r0, r0);
-  return g * sig;
+  return __builtin_fmaf(e, r0, r0);
+}
+
+__device__ inline float silu_exact(float g) { return g * (1.0f / (1.0f + __builtin_expf(-g))); }
+
+// In place: g[i] <- T(silu(g[i])) * u[i], i.e. y before its final rounding.
+template <class C>
+__device__ inline void swiglu_math(float (&g)[C::VEC], const float (&u)[C::VEC]) {
+  constexpr int VEC = C::VEC;
+  float mn = g[0];
+#pragma unroll
+  for (int i = 1; i < VEC; ++i) mn = __builtin_elementwise_minimum(mn, g[i]);
+  if (mn >= SiluConsts<C>::kFastMin) {  // false for NaN: exact path
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) g[i] = g[i] * recip_refined(1.0f + exp_neg_fast<C>(g[i]));
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) g[i] = silu_exact(g[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < VEC; i += 2) C::round2(g[i], g[i + 1]);
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) g[i] = g[i] * u[i];
 }
 
 template <class C>
@@ -36,8 +97,7 @@ __device__ inline u32x4 swiglu_vec(const u32x4& gw, const u32x4& uw) {
   float g[C::VEC], u[C::VEC];
   C::unpack(gw, g);
   C::unpack(uw, u);
-#pragma unroll
-  for (int i = 0; i < C::VEC; ++i) g[i] = C::round(silu(g[i])) * u[i];
+  swiglu_math<C>(g, u);
   return C::pack(g);
 }
 
@@ -52,16 +112,23 @@ __global__ __launch_bounds__(256) void swiglu_flat(const u32x4* __restrict__ gat
     for (int k = 0; k < UNROLL; ++k) {
       const int64_t v = base + k * 256;
       if (v < nvec) {
-        g[k] = __builtin_nontemporal_load(gate + v);
-        u[k] = __builtin_nontemporal_load(up + v);
+        g[k] = ld_stream(gate + v);
+        u[k] = ld_stream(up + v);
       }
     }
 #pragma unroll
     for (int k = 0; k < UNROLL; ++k) {
       const int64_t v = base + k * 256;
-      if (v < nvec) __builtin_nontemporal_store(swiglu_vec<C>(g[k], u[k]), y + v);
+      if (v < nvec) st_stream(swiglu_vec<C>(g[k], u[k]), y + v);
     }
   }
+}
+
+template <class C>
+__device__ inline float swiglu1(float g, float u) {
+  const float a = C::round(g >= SiluConsts<C>::kFastMin ? g * recip_refined(1.0f + exp_neg_fast<C>(g))
+                                                        : silu_exact(g));
+  return a * u;
 }
 
 template <class C>
@@ -70,20 +137,13 @@ __global__ __launch_bounds__(256) void swiglu_scalar(const void* __restrict__ ga
                                                      void* __restrict__ y, int64_t begin, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * 256;
   for (int64_t i = begin + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
-    C::store1(y, i, C::round(silu(C::load1(gate, i))) * C::load1(up, i));
+    C::store1(y, i, swiglu1<C>(C::load1(gate, i), C::load1(up, i)));
   }
 }
 
-template <class C>
-struct AmaxOp3 {
-  using type = MaxPkU16;
-};
-template <>
-struct AmaxOp3<CodecF32> {
-  using type = MaxU32;
-};
-
-// FP8 variant, register-resident rows. STATIC selects the static scale.
+// FP8 variant, register-resident rows; y is kept as floats (already rounded
+// to T) between the amax reduction and the quantisation. STATIC selects the
+// static scale.
 template <class C, int THREADS, int ITEMS, bool STATIC, int FMT>
 __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
     const void* __restrict__ gate, const void* __restrict__ up, uint8_t* __restrict__ yq,
@@ -97,19 +157,34 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
     const int64_t off = row * cols * C::kBytes;
     const u32x4* gr = reinterpret_cast<const u32x4*>(static_cast<const char*>(gate) + off);
     const u32x4* ur = reinterpret_cast<const u32x4*>(static_cast<const char*>(up) + off);
-    u32x4 yv[ITEMS];
-    uint32_t acc = 0;
+    u32x4 graw[ITEMS], uraw[ITEMS];
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       const int v = threadIdx.x + k * THREADS;
       if (v < nvec) {
-        yv[k] = swiglu_vec<C>(__builtin_nontemporal_load(gr + v), __builtin_nontemporal_load(ur + v));
-        acc = C::absmax_vec(yv[k], acc);
+        graw[k] = ld_stream(gr + v);
+        uraw[k] = ld_stream(ur + v);
       }
     }
-    acc = block_allreduce<NW>(acc, typename AmaxOp3<C>::type{}, lds, parity);
+    float y[ITEMS][VEC];
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+      const int v = threadIdx.x + k * THREADS;
+      if (v < nvec) {
+        float u[VEC];
+        C::unpack(graw[k], y[k]);
+        C::unpack(uraw[k], u);
+        swiglu_math<C>(y[k], u);
+#pragma unroll
+        for (int i = 0; i < VEC; i += 2) {
+          C::round2(y[k][i], y[k][i + 1]);
+          amax = absmax2(amax, y[k][i], y[k][i + 1]);
+        }
+      }
+    }
+    amax = bits_f32(block_allreduce<NW>(f32_bits(amax), MaxF32{}, lds, parity));
     parity ^= 1;
-    const float amax = C::absmax_to_float(acc);
     float s;
     if constexpr (STATIC) {
       s = static_scale;
@@ -124,18 +199,16 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
     for (int k = 0; k < ITEMS; ++k) {
       const int v = threadIdx.x + k * THREADS;
       if (v < nvec) {
-        float fy[VEC];
-        C::unpack(yv[k], fy);
         uint32_t wq[VEC / 4];
         if (fast) {
-          quant_fast<FMT, VEC>(fy, s, r, wq);
+          quant_fast<FMT, VEC>(y[k], s, r, wq);
         } else {
-          quant_exact<FMT, VEC>(fy, s, wq);
+          quant_exact<FMT, VEC>(y[k], s, wq);
         }
         if constexpr (VEC == 8) {
-          __builtin_nontemporal_store((u32x2){wq[0], wq[1]}, reinterpret_cast<u32x2*>(qr + (int64_t)v * 8));
+          st_stream((u32x2){wq[0], wq[1]}, reinterpret_cast<u32x2*>(qr + (int64_t)v * 8));
         } else {
-          __builtin_nontemporal_store(wq[0], reinterpret_cast<uint32_t*>(qr + (int64_t)v * 4));
+          st_stream(wq[0], reinterpret_cast<uint32_t*>(qr + (int64_t)v * 4));
         }
       }
     }
@@ -151,14 +224,13 @@ __global__ __launch_bounds__(256) void swiglu_fp8_generic(
   int parity = 0;
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const int64_t base = row * cols;
-    uint32_t acc = 0;
+    float amax = 0.0f;
     for (int64_t j = threadIdx.x; j < cols; j += 256) {
-      const float yv = C::round(C::round(silu(C::load1(gate, base + j))) * C::load1(up, base + j));
-      acc = max(acc, f32_bits(yv) & 0x7fffffffu);
+      const float yv = C::round(swiglu1<C>(C::load1(gate, base + j), C::load1(up, base + j)));
+      amax = absmax2(amax, yv, 0.0f);
     }
-    acc = block_allreduce<4>(acc, MaxU32{}, lds, parity);
+    amax = bits_f32(block_allreduce<4>(f32_bits(amax), MaxF32{}, lds, parity));
     parity ^= 1;
-    const float amax = bits_f32(acc);
     float s;
     if constexpr (STATIC) {
       s = static_scale;
@@ -169,7 +241,7 @@ __global__ __launch_bounds__(256) void swiglu_fp8_generic(
     const float r = 1.0f / s;
     const bool fast = fast_path_ok<FMT>(s, r, amax);
     for (int64_t j = threadIdx.x; j < cols; j += 256) {
-      const float yv = C::round(C::round(silu(C::load1(gate, base + j))) * C::load1(up, base + j));
+      const float yv = C::round(swiglu1<C>(C::load1(gate, base + j), C::load1(up, base + j)));
       const float qv = fast ? div_by_scale(yv, s, r) : div_x86(yv, s);
       yq[base + j] = (uint8_t)(fast ? (Fp8<FMT>::cvt4(qv, 0.0f, 0.0f, 0.0f) & 0xffu) : Fp8<FMT>::encode(qv));
     }
@@ -183,26 +255,18 @@ int32_t launch_swiglu_fp8(const void* gate, const void* up, uint8_t* yq, float* 
                       host_aligned(yq, C::VEC);
   const int64_t nvec = cols / C::VEC;
   const unsigned g = row_grid(rows);
-#define CCK_SWF(T_, I_) \
-  swiglu_fp8_resident<C, T_, I_, STATIC, FMT><<<g, T_, 0, st>>>(gate, up, yq, scale, rows, cols, static_scale)
-  if (vec_ok && nvec <= 64) {
-    CCK_SWF(64, 1);
-  } else if (vec_ok && nvec <= 256) {
-    CCK_SWF(256, 1);
-  } else if (vec_ok && nvec <= 512) {
-    CCK_SWF(256, 2);
-  } else if (vec_ok && nvec <= 1024) {
-    CCK_SWF(256, 4);
-  } else if (vec_ok && nvec <= 1792) {
-    CCK_SWF(256, 7);
-  } else if (vec_ok && nvec <= 2048) {
-    CCK_SWF(256, 8);
-  } else if (vec_ok && nvec <= 4096) {
-    CCK_SWF(512, 8);
-  } else {
+  auto run = [&](auto shape) {
+    using S = decltype(shape);
+    swiglu_fp8_resident<C, S::kThreads, S::kItems, STATIC, FMT><<<g, S::kThreads, 0, st>>>(
+        gate, up, yq, scale, rows, cols, static_scale);
+  };
+  // At most two vectors per thread keeps the kernel under 64 VGPRs of row
+  // state; 1024-thread rows measured fastest on MI355X at cols = 14336 bf16.
+  const bool done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
+                                             RowShape<512, 2>, RowShape<1024, 2>, RowShape<1024, 4>>(nvec, run);
+  if (!done) {
     swiglu_fp8_generic<C, STATIC, FMT><<<g, 256, 0, st>>>(gate, up, yq, scale, rows, cols, static_scale);
   }
-#undef CCK_SWF
   return launch_status();
 }
 
@@ -222,7 +286,7 @@ extern "C" int32_t launch_swiglu_fwd(const void* gate, const void* up, void* y, 
     if (vec_ok) {
       const int64_t nvec = n / C::VEC;
       if (nvec > 0) {
-        constexpr int UNROLL = 2;
+        constexpr int UNROLL = 4;
         const unsigned g = flat_grid((nvec + UNROLL - 1) / UNROLL, 256, 1 << 20);
         swiglu_flat<C, UNROLL><<<g, 256, 0, st>>>(static_cast<const u32x4*>(gate),
                                                    static_cast<const u32x4*>(up),

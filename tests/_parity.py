@@ -40,6 +40,24 @@ def bits_equal(actual: torch.Tensor, expected: torch.Tensor) -> np.ndarray:
     return (ai == ei) | (np.isnan(a.float().numpy()) & np.isnan(e.float().numpy()))
 
 
+# Per storage type: (one ulp relative, hard cap, allowed fraction above one ulp).
+# An element above one ulp comes from eager's double rounding: when the fp32
+# intermediate sits within an fp32 ulp of a rounding midpoint of the storage
+# type, a one-ulp difference in that intermediate becomes up to two ulps in
+# the next product (e.g. T(normed) * weight).
+ULP_TOL = {
+    torch.bfloat16: (2.0 ** -7, 2.0 ** -6, 1e-6),
+    torch.float16: (2.0 ** -10, 2.0 ** -9, 1e-5),
+    torch.float32: (1e-5, 1e-5, 0.0),
+}
+
+
+def assert_ulp_close(actual: torch.Tensor, expected: torch.Tensor, what: str) -> dict:
+    rel, hard, frac = ULP_TOL[expected.dtype]
+    assert_within_rel(actual, expected, hard, what + " (hard cap)")
+    return assert_within_rel(actual, expected, rel, what, max_outlier_fraction=frac)
+
+
 def assert_within_rel(actual: torch.Tensor, expected: torch.Tensor, rel: float, what: str,
                       max_outlier_fraction: float = 0.0, atol: float = 0.0) -> dict:
     """|actual - expected| <= rel * max(|actual|, |expected|) + atol elementwise,

@@ -1,0 +1,205 @@
+"""The C-ABI boundary and the validating binding, on the CPU.
+
+* libcustom_kernels_amd.so loads and exports every function that
+  include/custom_kernels_amd.h declares, with that header's argument count;
+* launchers return 0 for empty work and hipErrorInvalidValue (1) for an
+  unknown dtype / format / mode tag, in both cases before any device call
+  (reference csrc/kernels/rmsnorm_residual.cu:87-89, 113-114);
+* the binding mirrors the reference's Rust checks (src/kernels/tensor.rs,
+  error.rs, <op>.rs): ValueError for device type, contiguity, dtype, shape and
+  format errors, in the reference's order. Tensors are stood in for by
+  attribute-only fakes, so every case fails validation before a launch.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+from tests import _cck
+
+from custom_cuda_kernals_amd._lib import native  # noqa: E402
+from custom_cuda_kernals_amd import kernels  # noqa: E402
+
+
+def test_library_exports_every_declared_symbol():
+    decls = _cck.declared_functions()
+    assert len(decls) >= 11
+    lib = ctypes.CDLL(_cck.LIB_PATH)
+    for name in decls:
+        assert hasattr(lib, name), name
+
+
+def test_reference_launchers_are_declared_with_reference_arity():
+    d = _cck.declared_functions()
+    assert len(d["launch_rmsnorm_residual_fwd"]) == 10
+    assert len(d["launch_swiglu_fwd"]) == 6
+    assert len(d["launch_rope_fwd"]) == 13
+    assert len(d["launch_fp8_quant_block_fwd"]) == 8
+    assert len(d["launch_fp8_quant_tensor_fwd"]) == 9
+
+
+def test_empty_work_returns_success_without_device_calls():
+    lib = _cck.load()
+    assert lib.launch_rmsnorm_residual_fwd(None, None, None, None, None, 0, 4096, 1e-5, 2, None) == 0
+    assert lib.launch_rmsnorm_residual_fwd(None, None, None, None, None, 8, 0, 1e-5, 2, None) == 0
+    assert lib.launch_swiglu_fwd(None, None, None, 0, 2, None) == 0
+    assert lib.launch_rope_fwd(None, None, None, None, None, None, 0, 16, 8, 8, 64, 2, None) == 0
+    assert lib.launch_fp8_quant_block_fwd(None, None, None, 0, 16, 2, 3, None) == 0
+    assert lib.launch_fp8_quant_tensor_fwd(None, None, None, None, 16, 0, 2, 3, None) == 0
+    assert lib.launch_fp8_quant_token_fwd(None, None, None, 0, 16, 2, 3, None) == 0
+    assert lib.launch_fp8_quant_static_fwd(None, None, 0.05, 0, 16, 2, 3, None) == 0
+    assert lib.launch_rmsnorm_residual_fp8_fwd(None, None, None, None, None, None, 0, 16, 1e-5, 0.0, 0, 2, 3, None) == 0
+    assert lib.launch_swiglu_fp8_fwd(None, None, None, None, 0, 16, 0.0, 0, 2, 3, None) == 0
+
+
+def test_unknown_tags_return_invalid_value_before_device_calls():
+    lib = _cck.load()
+    assert lib.launch_rmsnorm_residual_fwd(None, None, None, None, None, 4, 8, 1e-5, 9, None) == 1
+    assert lib.launch_swiglu_fwd(None, None, None, 8, 3, None) == 1  # fp8 is not a compute dtype
+    assert lib.launch_rope_fwd(None, None, None, None, None, None, 1, 4, 2, 1, 8, 7, None) == 1
+    assert lib.launch_rope_fwd(None, None, None, None, None, None, 1, 4, 2, 1, 7, 2, None) == 1  # odd head_dim
+    assert lib.launch_fp8_quant_block_fwd(None, None, None, 4, 8, 2, 2, None) == 1  # bad fp8 format
+    assert lib.launch_fp8_quant_token_fwd(None, None, None, 4, 8, 5, 3, None) == 1
+    assert lib.launch_fp8_quant_tensor_fwd(None, None, None, None, 4, 8, 2, 9, None) == 1
+    assert lib.launch_fp8_quant_static_fwd(None, None, 0.05, 4, 8, 2, 0, None) == 1
+    assert lib.launch_rmsnorm_residual_fp8_fwd(None, None, None, None, None, None, 4, 8, 1e-5, 0.0, 2, 2, 3, None) == 1
+    assert lib.launch_swiglu_fp8_fwd(None, None, None, None, 4, 8, 0.0, 7, 2, 3, None) == 1
+    assert lib.cck_fp8_cvt_selftest(0, 16, 1, None, None) == 1
+
+
+class _Dev:
+    def __init__(self, type_="cuda", index=0):
+        self.type, self.index = type_, index
+
+
+class FakeTensor:
+    """Quacks like a torch.Tensor for the attributes the binding reads."""
+
+    def __init__(self, shape, dtype=torch.bfloat16, device="cuda", contiguous=True):
+        self.shape = torch.Size(shape)
+        self.dtype = dtype
+        self.device = _Dev(device)
+        self._contig = contiguous
+
+    def is_contiguous(self):
+        return self._contig
+
+    def data_ptr(self):
+        return 0
+
+
+def F(*shape, **kw):
+    return FakeTensor(shape, **kw)
+
+
+def _raises(fn, *args, match=None):
+    with pytest.raises(ValueError, match=match):
+        fn(*args)
+
+
+def test_device_then_contiguity_then_dtype_order():
+    # device type is checked first, even when the tensor is also non-contiguous
+    _raises(native.swiglu_fwd, F(4, 8, device="cpu", contiguous=False), F(4, 8), F(4, 8), match="must be a CUDA tensor")
+    _raises(native.swiglu_fwd, F(4, 8, contiguous=False), F(4, 8), F(4, 8), match="'gate' must be contiguous")
+    _raises(native.swiglu_fwd, F(4, 8, dtype=torch.int64), F(4, 8), F(4, 8), match="unsupported dtype 'torch.int64'")
+    # arguments are validated in order: a bad 'up' is reported before a bad 'y'
+    _raises(native.swiglu_fwd, F(4, 8), F(4, 8, device="cpu"), F(4, 8, contiguous=False), match="'up' must be a CUDA")
+
+
+def test_real_cpu_tensors_are_rejected_by_the_python_api():
+    with pytest.raises(ValueError, match="must be a CUDA tensor, got device type 'cpu'"):
+        kernels.swiglu(torch.randn(2, 8), torch.randn(2, 8))
+    with pytest.raises(ValueError):
+        kernels.rmsnorm_residual(torch.randn(2, 4, 8), torch.randn(2, 4, 8), torch.randn(8))
+    with pytest.raises(ValueError):
+        kernels.fp8_quant(torch.randn(4, 8), "e4m3", "block")
+    with pytest.raises(ValueError):
+        kernels.rope(torch.randn(1, 4, 2, 8), torch.randn(1, 4, 1, 8), torch.randn(4, 4), torch.randn(4, 4))
+
+
+def test_rmsnorm_checks():
+    ok = dict(x=F(2, 3, 8), r=F(2, 3, 8), w=F(8), y=F(2, 3, 8), ro=F(2, 3, 8))
+    def call(**over):
+        a = {**ok, **over}
+        native.rmsnorm_residual_fwd(a["x"], a["r"], a["w"], a["y"], a["ro"], 1e-6)
+    with pytest.raises(ValueError, match="dtype mismatch: 'residual' is F32 but expected BF16"):
+        call(r=F(2, 3, 8, dtype=torch.float32))
+    with pytest.raises(ValueError, match="'weight' is F16"):
+        call(w=F(8, dtype=torch.float16))
+    with pytest.raises(ValueError, match="shape mismatch: x/residual/y/residual_out must share"):
+        call(y=F(2, 3, 9))
+    with pytest.raises(ValueError, match=r"weight shape \[9\] must be \[8\]"):
+        call(w=F(9))
+    with pytest.raises(ValueError, match="at least 1 dimension"):
+        call(x=F(), r=F(), y=F(), ro=F(), w=F(1))
+
+
+def test_rope_checks():
+    ok = dict(q=F(1, 4, 2, 8), k=F(1, 4, 1, 8), c=F(4, 4, dtype=torch.float32), s=F(4, 4, dtype=torch.float32),
+              qo=F(1, 4, 2, 8), ko=F(1, 4, 1, 8))
+    def call(**over):
+        a = {**ok, **over}
+        native.rope_fwd(a["q"], a["k"], a["c"], a["s"], a["qo"], a["ko"])
+    with pytest.raises(ValueError, match="cos must be float32"):
+        call(c=F(4, 4))
+    with pytest.raises(ValueError, match="q must be 4-D"):
+        call(q=F(4, 2, 8), qo=F(4, 2, 8))
+    with pytest.raises(ValueError, match="q_out must match"):
+        call(qo=F(1, 4, 2, 16))
+    with pytest.raises(ValueError, match="share batch/seq_len/head_dim"):
+        call(k=F(1, 5, 1, 8), ko=F(1, 5, 1, 8))
+    with pytest.raises(ValueError, match="head_dim must be even"):
+        call(q=F(1, 4, 2, 7), qo=F(1, 4, 2, 7), k=F(1, 4, 1, 7), ko=F(1, 4, 1, 7))
+    with pytest.raises(ValueError, match=r"cos/sin must have shape \[4, 4\]"):
+        call(c=F(4, 3, dtype=torch.float32))
+    with pytest.raises(ValueError, match="'k_out' is F16"):
+        call(ko=F(1, 4, 1, 8, dtype=torch.float16))
+
+
+def test_fp8_checks():
+    e4 = torch.float8_e4m3fn
+    with pytest.raises(ValueError, match="fp8_format must be 'e4m3' or 'e5m2', got \"e4m4\""):
+        native.fp8_quant_block_fwd(F(4, 8, device="cpu"), F(4, 8, dtype=e4), F(1, 1, dtype=torch.float32), "e4m4")
+    with pytest.raises(ValueError, match="does not match requested fp8_format"):
+        native.fp8_quant_block_fwd(F(4, 8), F(4, 8, dtype=torch.float8_e5m2), F(1, 1, dtype=torch.float32), "e4m3")
+    with pytest.raises(ValueError, match="scale must be float32"):
+        native.fp8_quant_block_fwd(F(4, 8), F(4, 8, dtype=e4), F(1, 1), "e4m3")
+    with pytest.raises(ValueError, match="x must be 2-D"):
+        native.fp8_quant_block_fwd(F(4, 8, 2), F(4, 8, 2, dtype=e4), F(1, 1, dtype=torch.float32), "e4m3")
+    with pytest.raises(ValueError, match=r"scale shape \[1, 1\] must be \[2, 1\]"):
+        native.fp8_quant_block_fwd(F(130, 8), F(130, 8, dtype=e4), F(1, 1, dtype=torch.float32), "e4m3")
+    with pytest.raises(ValueError, match="amax_scratch must be int32"):
+        native.fp8_quant_tensor_fwd(F(4, 8), F(4, 8, dtype=e4), F(1, dtype=torch.float32), F(1, dtype=torch.int64), "e4m3")
+    with pytest.raises(ValueError, match="exactly 1 element"):
+        native.fp8_quant_tensor_fwd(F(4, 8), F(4, 8, dtype=e4), F(1, dtype=torch.float32), F(2, dtype=torch.int32), "e4m3")
+    with pytest.raises(ValueError, match=r"scale shape \[3\] must be \[4\]"):
+        native.fp8_quant_token_fwd(F(4, 8), F(4, 8, dtype=e4), F(3, dtype=torch.float32), "e4m3")
+    with pytest.raises(ValueError, match="x_fp8 shape"):
+        native.fp8_quant_static_fwd(F(4, 8), F(4, 9, dtype=e4), 0.05, "e4m3")
+
+
+def test_fused_checks():
+    e4 = torch.float8_e4m3fn
+    with pytest.raises(ValueError, match="scale must be a float32 tensor"):
+        native.rmsnorm_residual_fp8_fwd(F(2, 8), F(2, 8), F(8), F(2, 8, dtype=e4), None, F(2, 8), 1e-5, "e4m3", None)
+    with pytest.raises(ValueError, match=r"scale shape \[3\] must be \[2\]"):
+        native.rmsnorm_residual_fp8_fwd(F(2, 8), F(2, 8), F(8), F(2, 8, dtype=e4), F(3, dtype=torch.float32), F(2, 8),
+                                        1e-5, "e4m3", None)
+    with pytest.raises(ValueError, match="y_fp8 dtype"):
+        native.swiglu_fp8_fwd(F(2, 8), F(2, 8), F(2, 8), None, "e4m3", 0.05)
+    with pytest.raises(ValueError, match="dtype mismatch: 'up'"):
+        native.swiglu_fp8_fwd(F(2, 8), F(2, 8, dtype=torch.float16), F(2, 8, dtype=e4), None, "e4m3", 0.05)
+    with pytest.raises(ValueError):
+        kernels.swiglu_fp8(torch.randn(2, 8), torch.randn(2, 8), "e4m3")
+    with pytest.raises(ValueError, match="fp8_format"):
+        kernels.rmsnorm_residual_fp8(torch.randn(2, 8), torch.randn(2, 8), torch.randn(8), fp8_format="x")
+
+
+def test_python_api_argument_errors():
+    with pytest.raises(ValueError, match="granularity must be"):
+        kernels.fp8_quant(torch.randn(4, 8), "e4m3", "row")
+    with pytest.raises(ValueError, match="static scale is per-tensor"):
+        kernels.fp8_quant(torch.randn(4, 8), "e4m3", "token", scale=0.1)

@@ -119,6 +119,12 @@ def test_unaligned_input_pointer(gran, dtype):
     _check(x_cpu, "e4m3", gran, x_dev=x_dev)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("cols", [64, 512, 1024, 2048, 4096, 8192, 16384, 32768, 65536])
+def test_every_row_shape_bucket(cols, dtype):
+    _check(inputs.randn((3, cols), dtype, seed=cols), "e4m3", "token")
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 def test_long_rows_use_looping_path(dtype):
     x = inputs.randn((5, 40000), dtype, seed=11)

@@ -81,6 +81,15 @@ def test_swiglu_fp8_small(shape, dtype, fmt, static):
     _check_swiglu(g, u, fmt, static)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("cols", [64, 512, 1024, 2048, 4096, 8192, 16384, 32768])
+def test_every_row_shape_bucket(cols, dtype):
+    x, r, w = inputs.rmsnorm_inputs(3, cols, dtype, seed=cols)
+    _check_rms(x, r, w, 1e-5, "e4m3", None)
+    g, u = inputs.swiglu_inputs(3, cols, dtype, seed=cols + 1)
+    _check_swiglu(g, u, "e4m3", None)
+
+
 def test_config3v_swiglu_fp8_full_size():
     g, u = inputs.swiglu_inputs(*inputs.CONFIG_SHAPES["swiglu"], torch.bfloat16, seed=0)
     _check_swiglu(g, u, "e4m3", None)

@@ -3,7 +3,9 @@ baselines/rmsnorm_residual.py:123-136).
 
 * residual_out: bit-exact (one rounding of x + residual);
 * y: within one ulp of the storage type relative (bf16 2^-7, fp16 2^-10) and
-  1e-5 relative in fp32; the fraction of bit-identical elements is printed.
+  1e-5 relative in fp32, with at most 1e-6 (bf16) / 1e-5 (fp16) of elements
+  allowed up to two ulps (tests/_parity.py ULP_TOL explains why); the
+  fraction of bit-identical elements is printed.
 Shapes: the reference's standard + edge cases (baselines/rmsnorm_residual.py:75-91)
 and the BASELINE config-2 workload at full size.
 """
@@ -15,12 +17,10 @@ import torch
 
 from custom_cuda_kernals_amd.kernels import rmsnorm_residual
 from oracle import eager, inputs
-from tests._parity import assert_within_rel, bits_equal
+from tests._parity import assert_ulp_close, assert_within_rel, bits_equal
 
 pytestmark = pytest.mark.gpu
 
-REL = {torch.float32: 1e-5, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
-OUTLIERS = 1e-6
 CASES = [(4, 128, 768), (2, 2048, 4096), (1, 4096, 4096), (3, 17, 4096), (2, 64, 100), (8, 1, 4096),
          (1, 8192, 2048), (0, 128, 4096), (1, 1, 128)]
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
@@ -34,7 +34,7 @@ def _run(x, r, w, eps, x_dev=None, r_dev=None):
     if x.numel() == 0:
         return None
     assert bits_equal(ro, ro_ref).all(), "residual_out must be bit-exact"
-    stats = assert_within_rel(y, y_ref, REL[x.dtype], "y", max_outlier_fraction=OUTLIERS)
+    stats = assert_ulp_close(y, y_ref, "y")
     print(f"\n{tuple(x.shape)} {x.dtype}: {stats}")
     return stats
 
@@ -65,6 +65,13 @@ def test_unaligned_and_long_rows(dtype):
     xd, rd = xb.cuda()[1:].view(3, 1000), rb.cuda()[1:].view(3, 1000)
     assert xd.data_ptr() % 16 != 0
     _run(x[:3, :1000].contiguous(), r[:3, :1000].contiguous(), w[:1000].contiguous(), 1e-5, xd, rd)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("cols", [64, 512, 1024, 2048, 4096, 8192, 16384, 32768])
+def test_every_row_shape_bucket(cols, dtype):
+    x, r, w = inputs.rmsnorm_inputs(5, cols, dtype, seed=cols)
+    _run(x, r, w, 1e-5)
 
 
 def test_rejections():
