@@ -46,6 +46,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
   constexpr int NW = THREADS / 64;
   constexpr int VEC = C::VEC;
   __shared__ uint32_t lds[2 * NW];
+  __shared__ float lds_sum[2 * NW * ITEMS];
   const int nvec = (int)(cols / VEC);
   const u32x4* wv = static_cast<const u32x4*>(w);
   auto load_row = [&](int64_t row, u32x4 (&xa)[ITEMS], u32x4 (&ra)[ITEMS]) {
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
   if constexpr (PF) {
     if ((int64_t)blockIdx.x < rows) load_row(blockIdx.x, xn, rn);
   }
-  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x, parity ^= 1) {
     const int64_t off = row * cols * C::kBytes;
     u32x4* ror = reinterpret_cast<u32x4*>(static_cast<char*>(ro) + off);
     u32x4 xa[ITEMS], ra[ITEMS];
@@ -93,10 +94,11 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
       load_row(row, xa, ra);
     }
     u32x4 rov[ITEMS];
-    float acc = 0.0f;
+    float part[ITEMS];
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       const int v = threadIdx.x + k * THREADS;
+      part[k] = 0.0f;
       if (v < nvec) {
         float fx[VEC], fr[VEC], fo[VEC];
         C::unpack(xa[k], fx);
@@ -107,11 +109,12 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
         st_stream(rov[k], ror + v);
         C::unpack(rov[k], fo);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) acc += fo[i] * fo[i];
+        for (int i = 0; i < VEC; ++i) part[k] += fo[i] * fo[i];
       }
     }
-    const float total = bits_f32(block_allreduce<NW>(f32_bits(acc), AddF32{}, lds, parity));
-    parity ^= 1;
+    // Shape-independent order: the plain and the FP8 variants (which use
+    // different shapes) produce the same residual_out -> y bits.
+    const float total = canonical_row_sum<NW, ITEMS>(part, lds_sum, parity);
     const float variance = total / (float)cols;
     const float inv = 1.0f / __builtin_sqrtf(variance + eps);
 
@@ -148,7 +151,6 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
         }
       }
       amax = bits_f32(block_allreduce<NW>(f32_bits(amax), MaxF32{}, lds, parity));
-      parity ^= 1;
       float s;
       if constexpr (MODE == 1) {
         s = scale_from_amax<FMT>(amax);

@@ -18,8 +18,9 @@
 // and 1/(1+e) = one v_rcp_f32 plus a Newton step. For bf16 inputs, th = -g*HI
 // is exact (8-bit g times a 16-bit HI), so only the tiny c = -g*LO*ln2 is
 // rounded; other input types split the product with an fma. Vectors with a
-// gate below the fast range (exp(-g) near overflow, sigmoid subnormal) use the
-// IEEE expf / division path.
+// gate outside the fast range (exp(-g) near overflow, sigmoid subnormal, the
+// first-order correction no longer within an ulp, inf / NaN) use the IEEE
+// expf / division path.
 #include "launch.hpp"
 
 namespace cck {
@@ -33,7 +34,7 @@ struct SiluConsts {
   static constexpr bool kExactHi = false;
   static constexpr float kHi = 1.44269502162933349609375f;  // RN32(log2 e)
   static constexpr float kLo = 1.925963033500011e-08f;       // log2 e - kHi
-  static constexpr float kFastMin = -87.0f;                  // sigmoid stays normal
+  static constexpr float kFastAbs = 87.0f;                   // sigmoid stays normal
 };
 template <>
 struct SiluConsts<CodecBF16> {
@@ -41,7 +42,7 @@ struct SiluConsts<CodecBF16> {
   static constexpr float kHi = 1.44268798828125f;
   static constexpr float kLoLn2 = 4.888495368504664e-06f;  // (log2 e - kHi) * ln 2
   // First-order correction 1 + c is within an ulp for |c| < 1e-4 (|g| < 20).
-  static constexpr float kFastMin = -20.0f;
+  static constexpr float kFastAbs = 20.0f;
 };
 
 constexpr float kLn2 = 0.693147182464599609375f;
@@ -73,13 +74,15 @@ __device__ inline float recip_refined(float d) {
 __device__ inline float silu_exact(float g) { return g * (1.0f / (1.0f + __builtin_expf(-g))); }
 
 // In place: g[i] <- T(silu(g[i])) * u[i], i.e. y before its final rounding.
+// The fast path needs every |g| <= kFastAbs (one v_maximum3_f32 per two
+// elements, NaN-propagating, so NaN and +-inf take the exact path too).
 template <class C>
 __device__ inline void swiglu_math(float (&g)[C::VEC], const float (&u)[C::VEC]) {
   constexpr int VEC = C::VEC;
-  float mn = g[0];
+  float mx = 0.0f;
 #pragma unroll
-  for (int i = 1; i < VEC; ++i) mn = __builtin_elementwise_minimum(mn, g[i]);
-  if (mn >= SiluConsts<C>::kFastMin) {  // false for NaN: exact path
+  for (int i = 0; i < VEC; i += 2) mx = absmax2(mx, g[i], g[i + 1]);
+  if (mx <= SiluConsts<C>::kFastAbs) {
 #pragma unroll
     for (int i = 0; i < VEC; ++i) g[i] = g[i] * recip_refined(1.0f + exp_neg_fast<C>(g[i]));
   } else {
@@ -126,8 +129,9 @@ __global__ __launch_bounds__(256) void swiglu_flat(const u32x4* __restrict__ gat
 
 template <class C>
 __device__ inline float swiglu1(float g, float u) {
-  const float a = C::round(g >= SiluConsts<C>::kFastMin ? g * recip_refined(1.0f + exp_neg_fast<C>(g))
-                                                        : silu_exact(g));
+  const float a = C::round(__builtin_fabsf(g) <= SiluConsts<C>::kFastAbs
+                               ? g * recip_refined(1.0f + exp_neg_fast<C>(g))
+                               : silu_exact(g));
   return a * u;
 }
 
