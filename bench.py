@@ -44,6 +44,12 @@ def _parse():
     p.add_argument("--ops", default="all", help="comma-separated op names, or 'all'")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline time budget")
+    p.add_argument("--no-graph", action="store_true",
+                   help="launch the timed steps eagerly instead of replaying a captured HIP graph "
+                        "(for counter-collection runs; includes host launch overhead)")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="also run a 256 MiB device-to-device torch copy, the reference kernel "
+                        "for scaling FETCH_SIZE / WRITE_SIZE counters")
     return p.parse_args()
 
 
@@ -149,13 +155,27 @@ def _ops(torch, native):
     return ops
 
 
-def _time_op(torch, op, steps, warmup):
+def _time_op(torch, op, steps, warmup, use_graph=True):
     nsets = max(2, math.ceil(ROTATE_BYTES / op.set_bytes))
     sets = [op.make_set() for _ in range(nsets)]
     torch.cuda.synchronize()
     for i in range(warmup):
         op.launch(sets[i % nsets])
     torch.cuda.synchronize()
+    if not use_graph:
+        stream = torch.cuda.current_stream()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(steps):
+            op.launch(sets[i % nsets])
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end)
+        us = ms * 1000.0 / steps
+        del sets
+        torch.cuda.empty_cache()
+        return {"workload": op.workload, "us": round(us, 3),
+                "GB_per_s": round(op.nbytes / (us * 1e-6) / 1e9, 1), "steps": steps, "graph": False}
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -211,6 +231,20 @@ def _cpu_baseline(budget_s: float):
                       f"median of {len(times)} runs over ~{budget_s:.0f}s, {med_s * 1e3:.3f} ms/run"}
 
 
+def _traffic(op_name):
+    """Measured HBM bytes per launch of `op_name` from the committed counter
+    summary (profiles/pmc_traffic.json, written from two rocprofv3 --pmc runs,
+    FETCH_SIZE and WRITE_SIZE, scaled by the same counters on a plain copy);
+    None when no summary covers the op."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data["ops"][op_name]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -233,8 +267,15 @@ def main():
     for op in ops:
         if wanted and op.name not in wanted:
             continue
-        results[op.name] = _time_op(torch, op, args.steps, args.warmup)
+        results[op.name] = _time_op(torch, op, args.steps, args.warmup, use_graph=not args.no_graph)
         print(f"# {op.name}: {results[op.name]}", file=sys.stderr, flush=True)
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("# copy calibration: 3 x torch copy_ of 268435456 bytes", file=sys.stderr, flush=True)
 
     head = results.get("rmsnorm_residual") or next(iter(results.values()))
     head_name = "rmsnorm_residual" if "rmsnorm_residual" in results else next(iter(results))
@@ -255,7 +296,7 @@ def main():
         "config": {"workload": head["workload"], "op": head_name, "global_batch": 8192, "seq_len": 1,
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBPS, 4), "traffic": None},
+                     "frac": round(achieved / PEAK_GBPS, 4), "traffic": _traffic(head_name)},
         "ops": results,
     }
     if not args.no_cpu_baseline:

@@ -145,6 +145,73 @@ __global__ __launch_bounds__(256) void swiglu_scalar(const void* __restrict__ ga
   }
 }
 
+// Static-scale FP8 variant: no row reduction is needed, so it streams like
+// swiglu_flat; each 16-byte vector takes the fast conversion when its own
+// max |y| * (1/s) is inside the fast range, the exact path otherwise.
+template <class C, int FMT, int UNROLL>
+__global__ __launch_bounds__(256) void swiglu_fp8_static_flat(const u32x4* __restrict__ gate,
+                                                             const u32x4* __restrict__ up,
+                                                             uint8_t* __restrict__ yq, float s,
+                                                             int64_t nvec) {
+  constexpr int VEC = C::VEC;
+  const float r = 1.0f / s;
+  const bool scale_ok = fast_path_ok<FMT>(s, r, 0.0f);
+  const int64_t stride = (int64_t)gridDim.x * 256 * UNROLL;
+  for (int64_t base = (int64_t)blockIdx.x * 256 * UNROLL + threadIdx.x; base < nvec; base += stride) {
+    u32x4 g[UNROLL], u[UNROLL];
+#pragma unroll
+    for (int k = 0; k < UNROLL; ++k) {
+      const int64_t v = base + k * 256;
+      if (v < nvec) {
+        g[k] = ld_stream(gate + v);
+        u[k] = ld_stream(up + v);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < UNROLL; ++k) {
+      const int64_t v = base + k * 256;
+      if (v < nvec) {
+        float y[VEC], uf[VEC];
+        C::unpack(g[k], y);
+        C::unpack(u[k], uf);
+        swiglu_math<C>(y, uf);
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < VEC; i += 2) {
+          C::round2(y[i], y[i + 1]);
+          amax = absmax2(amax, y[i], y[i + 1]);
+        }
+        uint32_t wq[VEC / 4];
+        if (scale_ok && amax * r <= Fp8<FMT>::kFastLimit) {
+          quant_fast<FMT, VEC>(y, s, r, wq);
+        } else {
+          quant_exact<FMT, VEC>(y, s, wq);
+        }
+        if constexpr (VEC == 8) {
+          st_stream((u32x2){wq[0], wq[1]}, reinterpret_cast<u32x2*>(yq + v * 8));
+        } else {
+          st_stream(wq[0], reinterpret_cast<uint32_t*>(yq + v * 4));
+        }
+      }
+    }
+  }
+}
+
+template <class C, int FMT>
+__global__ __launch_bounds__(256) void swiglu_fp8_static_scalar(const void* __restrict__ gate,
+                                                               const void* __restrict__ up,
+                                                               uint8_t* __restrict__ yq, float s,
+                                                               int64_t begin, int64_t n) {
+  const float r = 1.0f / s;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = begin + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+    const float yv = C::round(swiglu1<C>(C::load1(gate, i), C::load1(up, i)));
+    const bool fast = fast_path_ok<FMT>(s, r, __builtin_fabsf(yv));
+    const float qv = fast ? div_by_scale(yv, s, r) : div_x86(yv, s);
+    yq[i] = (uint8_t)(fast ? (Fp8<FMT>::cvt4(qv, 0.0f, 0.0f, 0.0f) & 0xffu) : Fp8<FMT>::encode(qv));
+  }
+}
+
 // FP8 variant, register-resident rows; y is kept as floats (already rounded
 // to T) between the amax reduction and the quantisation. STATIC selects the
 // static scale.
@@ -317,7 +384,23 @@ extern "C" int32_t launch_swiglu_fp8_fwd(const void* gate, const void* up, uint8
     return with_fp8(fp8_format, [&](auto f) {
       constexpr int FMT = decltype(f)::value;
       if (scale_mode == 0) return launch_swiglu_fp8<C, false, FMT>(gate, up, y_fp8, scale, rows, cols, 0.0f, st);
-      return launch_swiglu_fp8<C, true, FMT>(gate, up, y_fp8, nullptr, rows, cols, static_scale, st);
+      // Static scale: one flat stream over rows * cols elements.
+      const int64_t n = rows * cols;
+      int64_t done = 0;
+      if (host_aligned(gate, 16) && host_aligned(up, 16) && host_aligned(y_fp8, C::VEC)) {
+        const int64_t nvec = n / C::VEC;
+        if (nvec > 0) {
+          constexpr int UNROLL = 4;
+          swiglu_fp8_static_flat<C, FMT, UNROLL><<<flat_grid((nvec + UNROLL - 1) / UNROLL, 256, 1 << 20), 256, 0, st>>>(
+              static_cast<const u32x4*>(gate), static_cast<const u32x4*>(up), y_fp8, static_scale, nvec);
+        }
+        done = nvec * C::VEC;
+      }
+      if (done < n) {
+        swiglu_fp8_static_scalar<C, FMT><<<flat_grid(n - done, 256, 4096), 256, 0, st>>>(gate, up, y_fp8, static_scale,
+                                                                                         done, n);
+      }
+      return launch_status();
     });
   });
 }
