@@ -98,12 +98,12 @@ struct CodecBF16 {
     return (u32x4){pack2_bf16(f[0], f[1]), pack2_bf16(f[2], f[3]), pack2_bf16(f[4], f[5]),
                    pack2_bf16(f[6], f[7])};
   }
-  __device__ static float round(float v) { return bits_f32(pack2_bf16(v, 0.0f) << 16); }
-  // Round two values to bf16 with one v_cvt_pk_bf16_f32 (RNE) and widen back.
+  // RN to bf16, returned as the fp32 value: v_cvt_pk_bf16_f32 with a zero low
+  // half yields the widened value directly (one instruction).
+  __device__ static float round(float v) { return bits_f32(pack2_bf16(0.0f, v)); }
   __device__ static void round2(float& a, float& b) {
-    const uint32_t w = pack2_bf16(a, b);
-    a = bf16_lo(w);
-    b = bf16_hi(w);
+    a = round(a);
+    b = round(b);
   }
   __device__ static float load1(const void* p, int64_t i) {
     return bits_f32((uint32_t) static_cast<const uint16_t*>(p)[i] << 16);
@@ -332,8 +332,26 @@ struct Fp8<kF8E5M2> {
 
 // Dynamic scale from an amax: clamp(amax / FP8_MAX, min=1e-12) with NaN
 // propagating through the clamp as torch.clamp does (baselines/fp8_quant.py:169,175).
+// FP8_MAX = 7 * 2^k (448 = 7 * 2^6, 57344 = 7 * 2^13), so amax / FP8_MAX =
+// (amax * 2^-k) / 7 with an exact first step, and the division by 7 is the
+// fma-corrected product with RN(1/7), correctly rounded for normal quotients
+// (checked exhaustively against IEEE division on the device). Quotients too
+// small to be normal are clamped to 1e-12 anyway; +inf is patched.
 template <int FMT>
 __device__ inline float scale_from_amax(float amax) {
+  constexpr float kPow2 = Fp8<FMT>::kMax / 7.0f;
+  constexpr float kR7 = 1.0f / 7.0f;
+  const float a = amax * (1.0f / kPow2);
+  const float q0 = a * kR7;
+  const float e = __builtin_fmaf(-q0, 7.0f, a);
+  float s = __builtin_fmaf(e, kR7, q0);
+  s = (amax == __builtin_inff()) ? amax : s;
+  return (s < kMinScale) ? kMinScale : s;
+}
+
+// Reference form of the same scale (IEEE division), for the device self-test.
+template <int FMT>
+__device__ inline float scale_from_amax_ieee(float amax) {
   const float s = amax / Fp8<FMT>::kMax;
   return (s < kMinScale) ? kMinScale : s;
 }
@@ -380,6 +398,50 @@ __device__ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) ==
 #ifndef CCK_STREAM_NT_STORE
 #define CCK_STREAM_NT_STORE 1
 #endif
+// One row of a tensor, addressed by 32-bit byte offsets. RowBuf<true> is a
+// raw buffer resource (base and size in SGPRs, no per-lane 64-bit address
+// arithmetic, accesses past `bytes` read 0 / are dropped by the hardware range
+// check); RowBuf<false> is a plain global pointer. Which one a row kernel uses
+// was measured per kernel on MI355X. Rows are at most a few hundred KB here.
+constexpr int kBufDword3 = 0x00020000;  // gfx9 family: DATA_FORMAT_32, no swizzle
+constexpr int kBufLoadPolicy = CCK_STREAM_NT_LOAD ? 2 : 0;   // nt
+constexpr int kBufStorePolicy = CCK_STREAM_NT_STORE ? 2 : 0;  // nt
+
+template <bool RSRC>
+struct RowBuf;
+
+// Raw buffer resource: base and size in SGPRs, 32-bit lane offsets, hardware
+// range check.
+template <>
+struct RowBuf<true> {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ RowBuf(const void* base, uint32_t bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufDword3)) {}
+  __device__ u32x4 ld16(uint32_t off) const {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufLoadPolicy));
+  }
+  __device__ void st16(const u32x4& v, uint32_t off) const {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kBufStorePolicy);
+  }
+  __device__ void st8(const u32x2& v, uint32_t off) const {
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, kBufStorePolicy);
+  }
+  __device__ void st4(uint32_t v, uint32_t off) const {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kBufStorePolicy);
+  }
+};
+
+// The same interface over global pointers (callers guard the row end).
+template <>
+struct RowBuf<false> {
+  char* p;
+  __device__ RowBuf(const void* base, uint32_t) : p(static_cast<char*>(const_cast<void*>(base))) {}
+  __device__ u32x4 ld16(uint32_t off) const;
+  __device__ void st16(const u32x4& v, uint32_t off) const;
+  __device__ void st8(const u32x2& v, uint32_t off) const;
+  __device__ void st4(uint32_t v, uint32_t off) const;
+};
+
 template <class T>
 __device__ inline T ld_stream(const T* p) {
   if constexpr (CCK_STREAM_NT_LOAD) {
@@ -395,6 +457,19 @@ __device__ inline void st_stream(T v, T* p) {
   } else {
     *p = v;
   }
+}
+
+__device__ inline u32x4 RowBuf<false>::ld16(uint32_t off) const {
+  return ld_stream(reinterpret_cast<const u32x4*>(p + off));
+}
+__device__ inline void RowBuf<false>::st16(const u32x4& v, uint32_t off) const {
+  st_stream(v, reinterpret_cast<u32x4*>(p + off));
+}
+__device__ inline void RowBuf<false>::st8(const u32x2& v, uint32_t off) const {
+  st_stream(v, reinterpret_cast<u32x2*>(p + off));
+}
+__device__ inline void RowBuf<false>::st4(uint32_t v, uint32_t off) const {
+  st_stream(v, reinterpret_cast<uint32_t*>(p + off));
 }
 
 }  // namespace cck

@@ -76,16 +76,18 @@ __global__ __launch_bounds__(THREADS) void fp8_token_resident(const void* __rest
   __shared__ uint32_t lds[2 * NW];
   const int nvec = (int)(cols / C::VEC);
   int parity = 0;
+  // Buffer-resource row access (no per-lane 64-bit addressing): 6.6 vs 6.8 us
+  // at [2048, 4096] bf16 on MI355X.
+  const uint32_t row_bytes = (uint32_t)(cols * C::kBytes);
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
-    const u32x4* xr =
-        reinterpret_cast<const u32x4*>(static_cast<const char*>(x) + row * cols * C::kBytes);
+    const RowBuf<true> bx(static_cast<const char*>(x) + row * cols * C::kBytes, row_bytes);
     u32x4 raw[ITEMS];
     uint32_t acc = 0;
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
-      const int v = threadIdx.x + k * THREADS;
-      if (v < nvec) {
-        raw[k] = ld_stream(xr + v);
+      const uint32_t v = threadIdx.x + k * THREADS;
+      if (v < (uint32_t)nvec) {
+        raw[k] = bx.ld16(v * 16u);
         acc = C::absmax_vec(raw[k], acc);
       }
     }
@@ -96,11 +98,25 @@ __global__ __launch_bounds__(THREADS) void fp8_token_resident(const void* __rest
     const float r = 1.0f / s;
     if (threadIdx.x == 0) scale[row] = s;
     const bool fast = fast_path_ok<FMT>(s, r, amax);
-    uint8_t* qr = q + row * cols;
+    const RowBuf<true> bq(q + row * cols, (uint32_t)cols);
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
-      const int v = threadIdx.x + k * THREADS;
-      if (v < nvec) quant_vec<C, FMT>(raw[k], s, r, fast, qr, (int64_t)v * C::VEC);
+      const uint32_t v = threadIdx.x + k * THREADS;
+      if (v < (uint32_t)nvec) {
+        float f[C::VEC];
+        C::unpack(raw[k], f);
+        uint32_t w[C::VEC / 4];
+        if (fast) {
+          quant_fast<FMT, C::VEC>(f, s, r, w);
+        } else {
+          quant_exact<FMT, C::VEC>(f, s, w);
+        }
+        if constexpr (C::VEC == 8) {
+          bq.st8((u32x2){w[0], w[1]}, v * 8u);
+        } else {
+          bq.st4(w[0], v * 4u);
+        }
+      }
     }
   }
 }

@@ -6,7 +6,9 @@
 //                           against the exact software encoder for every
 //                           fp32 bit pattern in [start, start + count);
 //   cck_div_selftest      - div_by_scale (three-op division) against IEEE
-//                           division x / s for caller-given x and s sets.
+//                           division x / s for caller-given x and s sets;
+//   cck_scale_selftest    - scale_from_amax (fma-corrected / 7) against
+//                           clamp(amax / FP8_MAX, 1e-12) with IEEE division.
 #include "launch.hpp"
 
 namespace cck {
@@ -80,10 +82,44 @@ __global__ __launch_bounds__(256) void div_selftest(const float* __restrict__ xs
   if (checked) atomicAdd(&counters[4], checked);
 }
 
+// counters: [0] scale mismatches (bitwise, NaN == NaN), [1] lowest mismatching
+// amax bit pattern. amax = every non-negative fp32 pattern in [start, start+count).
+template <int FMT>
+__global__ __launch_bounds__(256) void scale_selftest(uint64_t start, uint64_t count,
+                                                      unsigned long long* counters) {
+  unsigned long long n = 0, lo = ~0ull;
+  const uint64_t stride = (uint64_t)gridDim.x * 256;
+  for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += stride) {
+    const uint32_t bits = (uint32_t)(start + i) & 0x7fffffffu;
+    const float amax = bits_f32(bits);
+    const float a = scale_from_amax<FMT>(amax), b = scale_from_amax_ieee<FMT>(amax);
+    const bool same = (f32_bits(a) == f32_bits(b)) || (a != a && b != b);
+    if (!same) {
+      n += 1;
+      lo = lo < bits ? lo : bits;
+    }
+  }
+  if (n) {
+    atomicAdd(&counters[0], n);
+    atomicMin(&counters[1], lo);
+  }
+}
+
 }  // namespace
 }  // namespace cck
 
 using namespace cck;
+
+extern "C" int32_t cck_scale_selftest(uint64_t start, uint64_t count, int32_t fp8_format,
+                                      unsigned long long* counters, void* stream) {
+  if (count == 0) return (int32_t)hipSuccess;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned g = flat_grid((int64_t)(count / 64), 256, 8192);
+  return with_fp8(fp8_format, [&](auto f) {
+    scale_selftest<decltype(f)::value><<<g, 256, 0, st>>>(start, count, counters);
+    return launch_status();
+  });
+}
 
 extern "C" int32_t cck_fp8_cvt_selftest(uint64_t start, uint64_t count, int32_t fp8_format,
                                         unsigned long long* counters, void* stream) {

@@ -120,6 +120,13 @@ int32_t cck_fp8_cvt_selftest(uint64_t start, uint64_t count, int32_t fp8_format,
 int32_t cck_div_selftest(const float* xs, int64_t nx, const float* ss, int64_t ns,
                          unsigned long long* counters, void* stream);
 
+/* Compares the dynamic-scale computation with clamp(amax / FP8_MAX, 1e-12) in
+ * IEEE division for amax = every non-negative fp32 pattern in [start,
+ * start + count) (sign bit cleared). counters: 2 x u64, [0] zeroed, [1] preset
+ * to UINT64_MAX. */
+int32_t cck_scale_selftest(uint64_t start, uint64_t count, int32_t fp8_format,
+                           unsigned long long* counters, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

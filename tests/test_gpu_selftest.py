@@ -4,9 +4,12 @@ run through the C ABI diagnostics (csrc/selftest.hip):
 * gfx950's v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32 against the exact encoder
   (itself pinned to torch's cast and to the oracle in test_oracle_fp8.py) for
   all 2^32 fp32 bit patterns;
-* the three-op division against IEEE division for every finite bf16 x and a
-  large set of scales (random mantissas, every dynamic scale a bf16 amax can
-  produce, and edge scales).
+* the three-op division against IEEE division for every finite bf16 / fp16 x
+  and random fp32 x over a large set of scales (random mantissas, every
+  dynamic scale a bf16 amax can produce, and edge scales);
+* the dynamic scale clamp(amax / FP8_MAX, 1e-12) computed with the exact
+  power-of-two step and the fma-corrected division by 7, against IEEE
+  division, for every non-negative fp32 amax (2^31 patterns incl. inf / NaN).
 """
 
 from __future__ import annotations
@@ -89,3 +92,15 @@ def test_fast_division_matches_ieee_division(xset):
         print(f"first bitwise mismatch: x={x!r} s={s!r}")
     assert c[4] > 10**9
     assert c[1] == 0 and c[2] == 0
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_dynamic_scale_matches_ieee_division_for_every_amax(fmt):
+    lib = _cck.load()
+    counters = torch.zeros(2, dtype=torch.int64, device="cuda")
+    counters[1] = -1
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.cck_scale_selftest(0, 1 << 31, FMT_TAG[fmt], counters.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    c = counters.cpu().numpy().view(np.uint64)
+    assert c[0] == 0, f"{c[0]} scale mismatches, lowest amax bits {hex(int(c[1]))}"
