@@ -47,6 +47,8 @@ def _parse():
     p.add_argument("--no-graph", action="store_true",
                    help="launch the timed steps eagerly instead of replaying a captured HIP graph "
                         "(for counter-collection runs; includes host launch overhead)")
+    p.add_argument("--block", action="store_true",
+                   help="also time the Llama-3-8B decoder block (eager / fused / fp8) at S=4096")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a 256 MiB device-to-device torch copy, the reference kernel "
                         "for scaling FETCH_SIZE / WRITE_SIZE counters")
@@ -231,6 +233,31 @@ def _cpu_baseline(budget_s: float):
                       f"median of {len(times)} runs over ~{budget_s:.0f}s, {med_s * 1e3:.3f} ms/run"}
 
 
+def _block_latency(torch):
+    """Llama-3-8B decoder block, B=1 S=4096 bf16, in the three variants of
+    custom_cuda_kernals_amd.llama_block (the reference's integration proof,
+    examples/llama_block.py, with an FP8 variant added)."""
+    from custom_cuda_kernals_amd.llama_block import LlamaBlock, block_latency_ms
+
+    torch.manual_seed(0)
+    seq = 4096
+    ref = LlamaBlock(seq, mode="eager").eval()
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(1, seq, 4096, dtype=torch.bfloat16, device="cuda", generator=g) * 0.02
+    out = {}
+    for mode in ("eager", "fused", "fp8"):
+        blk = ref if mode == "eager" else LlamaBlock(seq, mode=mode).eval()
+        if blk is not ref:
+            blk.load_state_dict(ref.state_dict())
+        out[mode] = block_latency_ms(blk, x)
+        print(f"# block {mode}: {out[mode]}", file=sys.stderr, flush=True)
+        if blk is not ref:
+            del blk
+    out["speedup_fused_vs_eager"] = round(out["eager"]["median_ms"] / out["fused"]["median_ms"], 3)
+    out["speedup_fp8_vs_eager"] = round(out["eager"]["median_ms"] / out["fp8"]["median_ms"], 3)
+    return out
+
+
 def _traffic(op_name):
     """Measured HBM bytes per launch of `op_name` from the committed counter
     summary (profiles/pmc_traffic.json, written from two rocprofv3 --pmc runs,
@@ -299,6 +326,8 @@ def main():
                      "frac": round(achieved / PEAK_GBPS, 4), "traffic": _traffic(head_name)},
         "ops": results,
     }
+    if args.block:
+        line["block"] = _block_latency(torch)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = _cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)

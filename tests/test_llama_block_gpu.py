@@ -1,0 +1,77 @@
+"""Integration caller: a Llama-3-8B decoder block on this library's kernels
+(custom_cuda_kernals_amd/llama_block.py) against the same block in plain torch
+ops, with identical weights - the reference's integration gate
+(examples/llama_block.py:271-283: rtol 1e-2, atol 2e-2, outlier fraction 1e-5)
+for the bf16 fused block; the FP8 block (FP8 GEMMs fed by the fused
+RMSNorm+FP8 / SwiGLU+FP8 outputs) is held to a relative-error bound."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from custom_cuda_kernals_amd.llama_block import LlamaBlock
+
+pytestmark = pytest.mark.gpu
+
+SEQ = 512
+
+
+def _blocks():
+    torch.manual_seed(0)
+    ref = LlamaBlock(SEQ, mode="eager").eval()
+    out = {"eager": ref}
+    for mode in ("fused", "fp8"):
+        blk = LlamaBlock(SEQ, mode=mode).eval()
+        blk.load_state_dict(ref.state_dict())
+        out[mode] = blk
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(1, SEQ, 4096, dtype=torch.bfloat16, device="cuda", generator=g) * 0.02
+    return out, x
+
+
+def _assert_close_with_outliers(actual, expected, rtol, atol, frac):
+    diff = (actual.double() - expected.double()).abs()
+    bad = diff > atol + rtol * expected.double().abs()
+    assert bad.float().mean().item() <= frac, f"{int(bad.sum())} elements beyond rtol {rtol} / atol {atol}"
+
+
+def test_fused_block_matches_eager_block():
+    blocks, x = _blocks()
+    with torch.no_grad():
+        ref = blocks["eager"](x)
+        out = blocks["fused"](x)
+    assert out.shape == ref.shape and out.dtype == torch.bfloat16
+    _assert_close_with_outliers(out, ref, 1e-2, 2e-2, 1e-5)
+
+
+def test_fp8_block_tracks_eager_block():
+    blocks, x = _blocks()
+    with torch.no_grad():
+        ref = blocks["eager"](x).float()
+        out = blocks["fp8"](x).float()
+        resid = x.float()
+    assert torch.isfinite(out).all()
+    # Relative error of the block's update (output - input): FP8 e4m3 carries
+    # 3 mantissa bits, so a few percent is the expected quantisation error.
+    upd_ref, upd = ref - resid, out - resid
+    rel = ((upd - upd_ref).norm() / upd_ref.norm()).item()
+    cos = torch.nn.functional.cosine_similarity(upd.flatten(), upd_ref.flatten(), dim=0).item()
+    print(f"\nfp8 block: relative error of the update {rel:.4f}, cosine {cos:.6f}")
+    assert rel < 0.12 and cos > 0.995
+
+
+def test_fp8_block_activations_are_the_fused_kernels_codes():
+    """The FP8 block's first GEMM input is exactly rmsnorm_residual_fp8's
+    output, i.e. the quantisation of the fused bf16 block's normalised
+    activation (same kernels, same rows)."""
+    from custom_cuda_kernals_amd.kernels import fp8_quant, rmsnorm_residual, rmsnorm_residual_fp8
+
+    blocks, x = _blocks()
+    w = blocks["fp8"].input_layernorm_weight
+    zero = torch.zeros_like(x)
+    q, s, ro = rmsnorm_residual_fp8(x, zero, w, 1e-5)
+    y, ro2 = rmsnorm_residual(x, zero, w, 1e-5)
+    q2, s2 = fp8_quant(y.view(-1, y.shape[-1]), "e4m3", "token")
+    assert torch.equal(q.view(torch.uint8).view(-1, 4096), q2.view(torch.uint8))
+    assert torch.equal(s.view(-1), s2) and torch.equal(ro, ro2)
