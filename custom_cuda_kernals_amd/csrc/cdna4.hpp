@@ -276,11 +276,13 @@ __device__ inline float canonical_row_sum(const float (&part)[ITEMS], float* lds
 // quotient (valid for normal s, r and quotients; the exhaustive checks cover
 // the domains used here). The negated form makes signed zeros come out as
 // IEEE division's: x = -0 -> -0.
-__device__ inline float div_by_scale(float x, float s, float r) {
+__device__ inline float neg_div_by_scale(float x, float s, float r) {
   const float q0 = x * r;
   const float e = __builtin_fmaf(-q0, s, x);
-  return -__builtin_fmaf(-e, r, -q0);
+  return __builtin_fmaf(-e, r, -q0);  // -(x / s)
 }
+
+__device__ inline float div_by_scale(float x, float s, float r) { return -neg_div_by_scale(x, s, r); }
 
 // x / s with the NaN results of the x86 SSE/AVX division the CPU oracle (and
 // the reference's eager path) runs on: a NaN operand is returned quieted,
@@ -316,6 +318,12 @@ struct Fp8<kF8E4M3> {
     int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   }
+  // Codes of -a, -b, -c, -d (see cvt4_neg below).
+  __device__ static uint32_t cvt4_of_neg(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __builtin_bit_cast(int, a), false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return (uint32_t)w ^ 0x80808080u;
+  }
   __host__ __device__ static uint32_t encode(float v) { return encode_e4m3fn(v); }
 };
 
@@ -326,6 +334,11 @@ struct Fp8<kF8E5M2> {
   __device__ static uint32_t cvt4(float a, float b, float c, float d) {
     int w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
     return (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true);
+  }
+  __device__ static uint32_t cvt4_of_neg(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, __builtin_bit_cast(int, a), false);
+    w = __builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true);
+    return (uint32_t)w ^ 0x80808080u;
   }
   __host__ __device__ static uint32_t encode(float v) { return encode_e5m2(v); }
 };
@@ -367,13 +380,18 @@ __device__ inline bool fast_path_ok(float s, float r, float amax) {
 }
 
 // Quantise N values (N % 4 == 0) to N fp8 bytes packed little-endian into
-// N/4 words.
+// N/4 words. The quotients are formed negated (saving the negation per value)
+// and converted with cvt4_of_neg: an fp8 code's top bit is its sign and the
+// hardware conversion is sign-symmetric for every non-NaN fp32 (it matches the
+// sign-symmetric software encoders on every finite input, overflow codes
+// included), so flipping the four sign bits of the packed word gives the
+// codes of the true quotients. Inputs here are finite (fast_path_ok).
 template <int FMT, int N>
 __device__ inline void quant_fast(const float (&v)[N], float s, float r, uint32_t (&out)[N / 4]) {
 #pragma unroll
   for (int i = 0; i < N / 4; ++i) {
-    out[i] = Fp8<FMT>::cvt4(div_by_scale(v[4 * i], s, r), div_by_scale(v[4 * i + 1], s, r),
-                            div_by_scale(v[4 * i + 2], s, r), div_by_scale(v[4 * i + 3], s, r));
+    out[i] = Fp8<FMT>::cvt4_of_neg(neg_div_by_scale(v[4 * i], s, r), neg_div_by_scale(v[4 * i + 1], s, r),
+                                   neg_div_by_scale(v[4 * i + 2], s, r), neg_div_by_scale(v[4 * i + 3], s, r));
   }
 }
 
