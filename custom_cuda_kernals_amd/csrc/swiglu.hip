@@ -73,9 +73,22 @@ __device__ inline float recip_refined(float d) {
 
 __device__ inline float silu_exact(float g) { return g * (1.0f / (1.0f + __builtin_expf(-g))); }
 
+template <class C>
+__device__ inline float silu_fast(float g) {
+  return g * recip_refined(1.0f + exp_neg_fast<C>(g));
+}
+
+// SiLU of one element: the fast form inside its range, the exact form
+// elsewhere. Every path below computes exactly this per element, whatever
+// the neighbouring elements are.
+template <class C>
+__device__ inline float silu_one(float g) {
+  return __builtin_fabsf(g) <= SiluConsts<C>::kFastAbs ? silu_fast<C>(g) : silu_exact(g);
+}
+
 // In place: g[i] <- T(silu(g[i])) * u[i], i.e. y before its final rounding.
-// The fast path needs every |g| <= kFastAbs (one v_maximum3_f32 per two
-// elements, NaN-propagating, so NaN and +-inf take the exact path too).
+// A vector whose |g| are all <= kFastAbs (one v_maximum3_f32 per two
+// elements, NaN-propagating) takes the fast form without per-element selects.
 template <class C>
 __device__ inline void swiglu_math(float (&g)[C::VEC], const float (&u)[C::VEC]) {
   constexpr int VEC = C::VEC;
@@ -84,10 +97,10 @@ __device__ inline void swiglu_math(float (&g)[C::VEC], const float (&u)[C::VEC])
   for (int i = 0; i < VEC; i += 2) mx = absmax2(mx, g[i], g[i + 1]);
   if (mx <= SiluConsts<C>::kFastAbs) {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) g[i] = g[i] * recip_refined(1.0f + exp_neg_fast<C>(g[i]));
+    for (int i = 0; i < VEC; ++i) g[i] = silu_fast<C>(g[i]);
   } else {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) g[i] = silu_exact(g[i]);
+    for (int i = 0; i < VEC; ++i) g[i] = silu_one<C>(g[i]);
   }
 #pragma unroll
   for (int i = 0; i < VEC; i += 2) C::round2(g[i], g[i + 1]);
@@ -95,44 +108,133 @@ __device__ inline void swiglu_math(float (&g)[C::VEC], const float (&u)[C::VEC])
   for (int i = 0; i < VEC; ++i) g[i] = g[i] * u[i];
 }
 
-template <class C>
-__device__ inline u32x4 swiglu_vec(const u32x4& gw, const u32x4& uw) {
-  float g[C::VEC], u[C::VEC];
-  C::unpack(gw, g);
-  C::unpack(uw, u);
-  swiglu_math<C>(g, u);
-  return C::pack(g);
+// ---------------------------------------------------------------------------
+// bf16 SiLU table in LDS.
+//
+// A bf16 gate has only 2^16 values, so T(silu(g)) is a function of its 16
+// bits. The common range 2^-14 <= |g| < 32 (4864 values) is tabulated per
+// workgroup in LDS (19 KB of fp32, filled with silu_one at workgroup start),
+// which replaces the two transcendental instructions and the Newton step per
+// element by one ds_read_b32. Vectors with a gate outside the range (zeros,
+// tiny or huge values, inf/NaN) fall back to silu_one, so results are
+// bit-identical to the arithmetic path.
+//
+// Key of a bf16 pattern b with magnitude field m = b & 0x7fff and sign s:
+// 2 * (m - kLo) + s, i.e. the 16-bit pattern rotated left by one minus
+// 2 * kLo; two keys are formed per packed word with one v_pk_sub_u16.
+// ---------------------------------------------------------------------------
+struct SiluTableBF16 {
+  static constexpr uint32_t kLo = 0x3880;                    // 2^-14
+  static constexpr uint32_t kHi = 0x4200;                    // 32.0
+  static constexpr uint32_t kEntries = 2 * (kHi - kLo);      // 4864
+  static constexpr uint32_t kTinyKeys = 2 * (0x3b00 - kLo);  // |g| < 2^-9
+
+  // Rounded SiLU of every tabulated value. For |g| < 2^-9, sigmoid(g) =
+  // 1/2 + g/4 + O(g^3), so g*sigmoid(g) = (g/2)(1 + d) with |d| < 2^-10,
+  // inside half a bf16 ulp of the exactly representable g/2: those entries
+  // are g/2 without evaluating the SiLU (keys below kTinyKeys, a
+  // wave-uniform branch).
+  __device__ static void fill(float* tab, int tid, int nthreads) {
+    for (uint32_t i = tid; i < kEntries; i += nthreads) {
+      const uint32_t key = i + 2 * kLo;
+      const float g = bits_f32((((key & 1u) << 15) | (key >> 1)) << 16);
+      tab[i] = i < kTinyKeys ? g * 0.5f : CodecBF16::round(silu_one<CodecBF16>(g));
+    }
+  }
+
+  __device__ static uint32_t keys2(uint32_t w) {
+    const uint32_t rot = ((w << 1) & 0xfffefffeu) | ((w >> 15) & 0x00010001u);
+    const u16x2 k = __builtin_bit_cast(u16x2, rot) - (u16x2){(uint16_t)(2 * kLo), (uint16_t)(2 * kLo)};
+    return __builtin_bit_cast(uint32_t, k);
+  }
+
+  // a[i] <- T(silu(g[i])) for the 8 gates of w; false (a untouched) when any
+  // gate is outside the table.
+  __device__ static bool lookup8(const u32x4& w, const float* tab, float (&a)[8]) {
+    uint32_t key[4];
+    uint32_t mx = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      key[j] = keys2(w[j]);
+      mx = pk_max_u16(mx, key[j]);
+    }
+    if (max(mx & 0xffffu, mx >> 16) >= kEntries) return false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a[2 * j] = tab[key[j] & 0xffffu];
+      a[2 * j + 1] = tab[key[j] >> 16];
+    }
+    return true;
+  }
+};
+
+// T(silu(g[i])) for one 16-byte vector of gates, from the table when given.
+template <class C, bool TAB>
+__device__ inline void silu_vec(const u32x4& gw, const float* tab, float (&a)[C::VEC]) {
+  if constexpr (TAB) {
+    if (SiluTableBF16::lookup8(gw, tab, a)) return;
+  }
+  C::unpack(gw, a);
+  float mx = 0.0f;
+#pragma unroll
+  for (int i = 0; i < C::VEC; i += 2) mx = absmax2(mx, a[i], a[i + 1]);
+  if (mx <= SiluConsts<C>::kFastAbs) {
+#pragma unroll
+    for (int i = 0; i < C::VEC; ++i) a[i] = silu_fast<C>(a[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < C::VEC; ++i) a[i] = silu_one<C>(a[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < C::VEC; i += 2) C::round2(a[i], a[i + 1]);
 }
 
-template <class C, int UNROLL>
-__global__ __launch_bounds__(256) void swiglu_flat(const u32x4* __restrict__ gate,
-                                                   const u32x4* __restrict__ up,
-                                                   u32x4* __restrict__ y, int64_t nvec) {
-  const int64_t stride = (int64_t)gridDim.x * 256 * UNROLL;
-  for (int64_t base = (int64_t)blockIdx.x * 256 * UNROLL + threadIdx.x; base < nvec; base += stride) {
-    u32x4 g[UNROLL], u[UNROLL];
+// The plain op: a grid-stride stream of 16-byte vectors, UNROLL per thread
+// per step. With TAB (bf16), each workgroup first fills the SiLU table; the
+// loads of its first step are issued before the fill so they overlap it.
+template <class C, int THREADS, int UNROLL, bool TAB>
+__global__ __launch_bounds__(THREADS) void swiglu_flat(const u32x4* __restrict__ gate,
+                                                       const u32x4* __restrict__ up,
+                                                       u32x4* __restrict__ y, int64_t nvec) {
+  __shared__ float tab[TAB ? SiluTableBF16::kEntries : 1];
+  const int64_t stride = (int64_t)gridDim.x * THREADS * UNROLL;
+  int64_t base = (int64_t)blockIdx.x * THREADS * UNROLL + threadIdx.x;
+  u32x4 g[UNROLL], u[UNROLL];
+  auto load = [&](int64_t b) {
 #pragma unroll
     for (int k = 0; k < UNROLL; ++k) {
-      const int64_t v = base + k * 256;
+      const int64_t v = b + k * THREADS;
       if (v < nvec) {
         g[k] = ld_stream(gate + v);
         u[k] = ld_stream(up + v);
       }
     }
+  };
+  load(base);
+  if constexpr (TAB) {
+    SiluTableBF16::fill(tab, threadIdx.x, THREADS);
+    __syncthreads();
+  }
+  for (; base < nvec; base += stride) {
 #pragma unroll
     for (int k = 0; k < UNROLL; ++k) {
-      const int64_t v = base + k * 256;
-      if (v < nvec) st_stream(swiglu_vec<C>(g[k], u[k]), y + v);
+      const int64_t v = base + k * THREADS;
+      if (v < nvec) {
+        float a[C::VEC], uf[C::VEC];
+        silu_vec<C, TAB>(g[k], tab, a);
+        C::unpack(u[k], uf);
+#pragma unroll
+        for (int i = 0; i < C::VEC; ++i) a[i] = a[i] * uf[i];
+        st_stream(C::pack(a), y + v);
+      }
     }
+    load(base + stride);
   }
 }
 
 template <class C>
 __device__ inline float swiglu1(float g, float u) {
-  const float a = C::round(__builtin_fabsf(g) <= SiluConsts<C>::kFastAbs
-                               ? g * recip_refined(1.0f + exp_neg_fast<C>(g))
-                               : silu_exact(g));
-  return a * u;
+  return C::round(silu_one<C>(g)) * u;
 }
 
 template <class C>
@@ -148,36 +250,46 @@ __global__ __launch_bounds__(256) void swiglu_scalar(const void* __restrict__ ga
 // Static-scale FP8 variant: no row reduction is needed, so it streams like
 // swiglu_flat; each 16-byte vector takes the fast conversion when its own
 // max |y| * (1/s) is inside the fast range, the exact path otherwise.
-template <class C, int FMT, int UNROLL>
-__global__ __launch_bounds__(256) void swiglu_fp8_static_flat(const u32x4* __restrict__ gate,
-                                                             const u32x4* __restrict__ up,
-                                                             uint8_t* __restrict__ yq, float s,
-                                                             int64_t nvec) {
+template <class C, int FMT, int THREADS, int UNROLL, bool TAB>
+__global__ __launch_bounds__(THREADS) void swiglu_fp8_static_flat(const u32x4* __restrict__ gate,
+                                                                 const u32x4* __restrict__ up,
+                                                                 uint8_t* __restrict__ yq, float s,
+                                                                 int64_t nvec) {
   constexpr int VEC = C::VEC;
+  __shared__ float tab[TAB ? SiluTableBF16::kEntries : 1];
   const float r = 1.0f / s;
   const bool scale_ok = fast_path_ok<FMT>(s, r, 0.0f);
-  const int64_t stride = (int64_t)gridDim.x * 256 * UNROLL;
-  for (int64_t base = (int64_t)blockIdx.x * 256 * UNROLL + threadIdx.x; base < nvec; base += stride) {
-    u32x4 g[UNROLL], u[UNROLL];
+  const int64_t stride = (int64_t)gridDim.x * THREADS * UNROLL;
+  int64_t base = (int64_t)blockIdx.x * THREADS * UNROLL + threadIdx.x;
+  u32x4 g[UNROLL], u[UNROLL];
+  auto load = [&](int64_t b) {
 #pragma unroll
     for (int k = 0; k < UNROLL; ++k) {
-      const int64_t v = base + k * 256;
+      const int64_t v = b + k * THREADS;
       if (v < nvec) {
         g[k] = ld_stream(gate + v);
         u[k] = ld_stream(up + v);
       }
     }
+  };
+  load(base);
+  if constexpr (TAB) {
+    SiluTableBF16::fill(tab, threadIdx.x, THREADS);
+    __syncthreads();
+  }
+  for (; base < nvec; base += stride) {
 #pragma unroll
     for (int k = 0; k < UNROLL; ++k) {
-      const int64_t v = base + k * 256;
+      const int64_t v = base + k * THREADS;
       if (v < nvec) {
         float y[VEC], uf[VEC];
-        C::unpack(g[k], y);
+        silu_vec<C, TAB>(g[k], tab, y);
         C::unpack(u[k], uf);
-        swiglu_math<C>(y, uf);
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < VEC; i += 2) {
+          y[i] = y[i] * uf[i];
+          y[i + 1] = y[i + 1] * uf[i + 1];
           C::round2(y[i], y[i + 1]);
           amax = absmax2(amax, y[i], y[i + 1]);
         }
@@ -194,6 +306,7 @@ __global__ __launch_bounds__(256) void swiglu_fp8_static_flat(const u32x4* __res
         }
       }
     }
+    load(base + stride);
   }
 }
 
@@ -214,24 +327,26 @@ __global__ __launch_bounds__(256) void swiglu_fp8_static_scalar(const void* __re
 
 // FP8 variant, register-resident rows; y is kept as floats (already rounded
 // to T) between the amax reduction and the quantisation. STATIC selects the
-// static scale.
-template <class C, int THREADS, int ITEMS, bool STATIC, int FMT>
+// static scale; TAB (bf16) the LDS SiLU table, filled while the first row's
+// loads are in flight.
+template <class C, int THREADS, int ITEMS, bool STATIC, int FMT, bool TAB>
 __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
     const void* __restrict__ gate, const void* __restrict__ up, uint8_t* __restrict__ yq,
     float* __restrict__ scale, int64_t rows, int64_t cols, float static_scale) {
   constexpr int NW = THREADS / 64;
   constexpr int VEC = C::VEC;
   __shared__ uint32_t lds[2 * NW];
+  __shared__ float tab[TAB ? SiluTableBF16::kEntries : 1];
   const int nvec = (int)(cols / VEC);
   int parity = 0;
   // Global-pointer row access: for this kernel's 1024 x 2 shape it measured
   // faster than buffer resources on MI355X (96 vs 119 us at [8192, 14336]).
   const uint32_t row_bytes = (uint32_t)(cols * C::kBytes);
-  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+  u32x4 graw[ITEMS], uraw[ITEMS];
+  auto load = [&](int64_t row) {
     const int64_t off = row * cols * C::kBytes;
     const RowBuf<false> bg(static_cast<const char*>(gate) + off, row_bytes);
     const RowBuf<false> bu(static_cast<const char*>(up) + off, row_bytes);
-    u32x4 graw[ITEMS], uraw[ITEMS];
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       const uint32_t v = threadIdx.x + k * THREADS;
@@ -240,6 +355,14 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
         uraw[k] = bu.ld16(v * 16u);
       }
     }
+  };
+  int64_t row = blockIdx.x;
+  if (row < rows) load(row);
+  if constexpr (TAB) {
+    SiluTableBF16::fill(tab, threadIdx.x, THREADS);
+    __syncthreads();
+  }
+  for (; row < rows; row += gridDim.x) {
     float y[ITEMS][VEC];
     float amax = 0.0f;
 #pragma unroll
@@ -247,11 +370,12 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
       const int v = threadIdx.x + k * THREADS;
       if (v < nvec) {
         float u[VEC];
-        C::unpack(graw[k], y[k]);
+        silu_vec<C, TAB>(graw[k], tab, y[k]);
         C::unpack(uraw[k], u);
-        swiglu_math<C>(y[k], u);
 #pragma unroll
         for (int i = 0; i < VEC; i += 2) {
+          y[k][i] = y[k][i] * u[i];
+          y[k][i + 1] = y[k][i + 1] * u[i + 1];
           C::round2(y[k][i], y[k][i + 1]);
           amax = absmax2(amax, y[k][i], y[k][i + 1]);
         }
@@ -287,6 +411,7 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
         }
       }
     }
+    if (row + gridDim.x < rows) load(row + gridDim.x);
   }
 }
 
@@ -332,7 +457,9 @@ int32_t launch_swiglu_fp8(const void* gate, const void* up, uint8_t* yq, float* 
   const unsigned g = row_grid(rows);
   auto run = [&](auto shape) {
     using S = decltype(shape);
-    swiglu_fp8_resident<C, S::kThreads, S::kItems, STATIC, FMT><<<g, S::kThreads, 0, st>>>(
+    // The table pays for its per-workgroup fill only on long rows.
+    constexpr bool kTab = std::is_same_v<C, CodecBF16> && S::kThreads == 1024;
+    swiglu_fp8_resident<C, S::kThreads, S::kItems, STATIC, FMT, kTab><<<g, S::kThreads, 0, st>>>(
         gate, up, yq, scale, rows, cols, static_scale);
   };
   // At most two vectors per thread keeps the kernel under 64 VGPRs of row
@@ -344,6 +471,12 @@ int32_t launch_swiglu_fp8(const void* gate, const void* up, uint8_t* yq, float* 
   }
   return launch_status();
 }
+
+// Streams of at least this many 16-byte vectors (1M bf16 elements) use the
+// SiLU table: 1024-thread workgroups of two vectors per thread, so one table
+// fill serves 16384 elements.
+constexpr int64_t kTabMinVec = int64_t(1) << 17;
+constexpr int kTabThreads = 1024, kTabUnroll = 2;
 
 }  // namespace
 }  // namespace cck
@@ -360,12 +493,22 @@ extern "C" int32_t launch_swiglu_fwd(const void* gate, const void* up, void* y, 
     int64_t done = 0;
     if (vec_ok) {
       const int64_t nvec = n / C::VEC;
-      if (nvec > 0) {
+      const u32x4* g4 = static_cast<const u32x4*>(gate);
+      const u32x4* u4 = static_cast<const u32x4*>(up);
+      u32x4* y4 = static_cast<u32x4*>(y);
+      bool tab = false;
+      if constexpr (std::is_same_v<C, CodecBF16>) {
+        if (nvec >= kTabMinVec) {
+          constexpr int kPer = kTabThreads * kTabUnroll;
+          swiglu_flat<C, kTabThreads, kTabUnroll, true>
+              <<<flat_grid((nvec + kPer - 1) / kPer, 1, 1 << 20), kTabThreads, 0, st>>>(g4, u4, y4, nvec);
+          tab = true;
+        }
+      }
+      if (!tab && nvec > 0) {
         constexpr int UNROLL = 4;
-        const unsigned g = flat_grid((nvec + UNROLL - 1) / UNROLL, 256, 1 << 20);
-        swiglu_flat<C, UNROLL><<<g, 256, 0, st>>>(static_cast<const u32x4*>(gate),
-                                                   static_cast<const u32x4*>(up),
-                                                   static_cast<u32x4*>(y), nvec);
+        swiglu_flat<C, 256, UNROLL, false>
+            <<<flat_grid((nvec + UNROLL - 1) / UNROLL, 256, 1 << 20), 256, 0, st>>>(g4, u4, y4, nvec);
       }
       done = nvec * C::VEC;
     }
@@ -393,10 +536,23 @@ extern "C" int32_t launch_swiglu_fp8_fwd(const void* gate, const void* up, uint8
       int64_t done = 0;
       if (host_aligned(gate, 16) && host_aligned(up, 16) && host_aligned(y_fp8, C::VEC)) {
         const int64_t nvec = n / C::VEC;
-        if (nvec > 0) {
+        const u32x4* g4 = static_cast<const u32x4*>(gate);
+        const u32x4* u4 = static_cast<const u32x4*>(up);
+        bool tab = false;
+        if constexpr (std::is_same_v<C, CodecBF16>) {
+          if (nvec >= kTabMinVec) {
+            constexpr int kPer = kTabThreads * kTabUnroll;
+            swiglu_fp8_static_flat<C, FMT, kTabThreads, kTabUnroll, true>
+                <<<flat_grid((nvec + kPer - 1) / kPer, 1, 1 << 20), kTabThreads, 0, st>>>(g4, u4, y_fp8,
+                                                                                          static_scale, nvec);
+            tab = true;
+          }
+        }
+        if (!tab && nvec > 0) {
           constexpr int UNROLL = 4;
-          swiglu_fp8_static_flat<C, FMT, UNROLL><<<flat_grid((nvec + UNROLL - 1) / UNROLL, 256, 1 << 20), 256, 0, st>>>(
-              static_cast<const u32x4*>(gate), static_cast<const u32x4*>(up), y_fp8, static_scale, nvec);
+          swiglu_fp8_static_flat<C, FMT, 256, UNROLL, false>
+              <<<flat_grid((nvec + UNROLL - 1) / UNROLL, 256, 1 << 20), 256, 0, st>>>(g4, u4, y_fp8, static_scale,
+                                                                                      nvec);
         }
         done = nvec * C::VEC;
       }

@@ -110,3 +110,19 @@ def test_fused_rejections():
         rmsnorm_residual_fp8(x, x, torch.randn(8, device="cuda"), fp8_format="e3m4")
     with pytest.raises(ValueError):
         swiglu_fp8(x, torch.randn(4, 8, device="cuda", dtype=torch.float16))
+
+
+def test_every_bf16_gate_fused_table_rows():
+    """Rows of 16384 (the LDS-table resident kernel) holding every finite bf16
+    gate value, shuffled, with random up: codes and scales equal the
+    quantised unfused output, per-token and static."""
+    import numpy as np
+
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    bits[(bits & 0x7FFF) >= 0x7F80] = 0  # finite gates only, so row scales stay finite
+    g = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+    gen = torch.Generator().manual_seed(11)
+    g = g.repeat(4)[torch.randperm(4 << 16, generator=gen)].view(16, 16384)
+    u = torch.randn(16, 16384, generator=gen).to(torch.bfloat16)
+    for static in (None, 0.05):
+        _check_swiglu(g, u, "e4m3", static)

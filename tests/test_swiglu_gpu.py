@@ -3,7 +3,9 @@ baselines/swiglu.py:107-112): within one storage-type ulp relative (bf16
 2^-7, fp16 2^-10), 1e-5 relative in fp32 (rare two-ulp elements bounded as in
 tests/_parity.py ULP_TOL). Shapes: the reference's case table
 (baselines/swiglu.py:70-88), the vector-tail sizes n = 1..129 its kernel
-tests sweep (tests/test_swiglu_kernel.py:74-93), BASELINE config 3 at full size.
+tests sweep (tests/test_swiglu_kernel.py:74-93), BASELINE config 3 at full size,
+and every one of the 65536 bf16 gate values through both the LDS-table
+kernels (streams of >= 1M elements) and the arithmetic kernels.
 """
 
 from __future__ import annotations
@@ -13,7 +15,7 @@ import torch
 
 from custom_cuda_kernals_amd.kernels import swiglu
 from oracle import eager, inputs
-from tests._parity import assert_ulp_close, assert_within_rel
+from tests._parity import assert_ulp_close, assert_within_rel, bits_equal
 
 pytestmark = pytest.mark.gpu
 
@@ -64,3 +66,33 @@ def test_extreme_gate_values():
     assert torch.equal(torch.isnan(y), torch.isnan(y_ref))
     fin = ~torch.isnan(y_ref)
     assert_within_rel(y[fin], y_ref[fin], 1e-5, "extreme")
+
+
+def _every_bf16() -> torch.Tensor:
+    import numpy as np
+
+    return torch.from_numpy(np.arange(1 << 16, dtype=np.uint16).view(np.int16)).view(torch.bfloat16)
+
+
+def test_every_bf16_gate_table_equals_arithmetic():
+    """All 2^16 gate patterns (zeros, subnormals, inf, NaN included) with up = 1,
+    so y is the rounded SiLU itself. 16 shuffled copies (1M elements) take the
+    table kernel, with table and fallback vectors mixed in every wave; the
+    plain 2^16 copy takes the arithmetic kernel. The two must agree bit for
+    bit, and both stay within the ulp bound of the oracle."""
+    g = _every_bf16()
+    gen = torch.Generator().manual_seed(7)
+    perm = torch.randperm(16 << 16, generator=gen)
+    g_big = g.repeat(16)[perm]
+    y_big = swiglu(g_big.cuda(), torch.ones_like(g_big).cuda()).cpu()
+    y_small = swiglu(g.cuda(), torch.ones_like(g).cuda()).cpu()
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    y_back = y_big[inv].view(16, -1)
+    for c in range(16):
+        assert bits_equal(y_back[c], y_small).all(), f"copy {c}: table and arithmetic kernels differ"
+    y_ref = eager.swiglu(g, torch.ones_like(g))
+    nan = torch.isnan(y_ref)
+    assert torch.equal(torch.isnan(y_small), nan)
+    stats = assert_ulp_close(y_small[~nan], y_ref[~nan], "every bf16 gate")
+    print(f"\nevery bf16 gate vs oracle: {stats}")
