@@ -119,7 +119,15 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
     // Shape-independent order: the plain and the FP8 variants (which use
     // different shapes) produce the same residual_out -> y bits.
     const float total = canonical_row_sum<NW, ITEMS>(part, lds_sum, parity);
-    const float variance = total / (float)cols;
+    // Dividing by a power of two is exact scaling: the product with its
+    // reciprocal is the same correctly rounded quotient, without the IEEE
+    // division sequence (the common case; the branch is wave-uniform).
+    float variance;
+    if ((cols & (cols - 1)) == 0) {
+      variance = total * (1.0f / (float)cols);
+    } else {
+      variance = total / (float)cols;
+    }
     const float inv = 1.0f / __builtin_sqrtf(variance + eps);
 
     if constexpr (MODE == 0) {
