@@ -29,6 +29,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from custom_cuda_kernals_amd.fp8_format import fp8_linear
 from custom_cuda_kernals_amd.kernels import (
     fp8_quant,
     rmsnorm_residual,
@@ -92,16 +93,14 @@ def _eager_swiglu(gate, up):
 
 
 class _Fp8Linear:
-    """A bf16 weight [N, K] quantised once to e4m3fn per output channel."""
+    """A bf16 weight [N, K] quantised once to e4m3fn per output channel; the
+    activation comes per token (row-wise x row-wise _scaled_mm)."""
 
     def __init__(self, weight: torch.Tensor) -> None:
-        q, s = fp8_quant(weight.contiguous(), "e4m3", "token")
-        self.w_t = q.t()  # [K, N] column-major view, as _scaled_mm wants
-        self.scale = s.view(1, -1)
+        self.w_codes, self.w_scale = fp8_quant(weight.contiguous(), "e4m3", "token")
 
     def __call__(self, x_fp8: torch.Tensor, x_scale: torch.Tensor) -> torch.Tensor:
-        return torch._scaled_mm(x_fp8, self.w_t, scale_a=x_scale.view(-1, 1), scale_b=self.scale,
-                                out_dtype=torch.bfloat16)
+        return fp8_linear(x_fp8, x_scale, "token", self.w_codes, self.w_scale, "token")
 
 
 class LlamaBlock(nn.Module):
