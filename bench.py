@@ -154,6 +154,35 @@ def _ops(torch, native):
                   e5a * 7))
     ops.append(Op("swiglu_fp8_static_T16384", "chain_swiglu_fp8_static0.05_bf16_16384x14336", e5b * 5, mk5b,
                   lambda b: native.swiglu_fp8_fwd(b["g"], b["u"], b["q"], None, "e4m3", 0.05), e5b * 5))
+
+    # MoE dispatch (the reference's standard cases, baselines/token_permute.py:128-146 and
+    # baselines/moe_router.py:72-79): not BASELINE configs; reported beside them.
+    gs, gd, gh = 2048, 4096, 4096
+
+    def mkg():
+        return dict(src=rn(gs, gh), idx=torch.randint(0, gs, (gd,), device=dev, generator=g),
+                    dst=torch.empty(gd, gh, dtype=bf16, device=dev))
+
+    ops.append(Op("token_gather", "moe_gather_bf16_2048to4096x4096", gd * gh * 4 + gd * 8, mkg,
+                  lambda b: native.token_gather_fwd(b["src"], b["idx"], b["dst"]), gs * gh * 2 + gd * gh * 2))
+    for ck in (2, 6):
+        ct, ch = 2048, 4096
+
+        def mkc(ck=ck, ct=ct, ch=ch):
+            return dict(eo=rn(ct * ck, ch), ui=torch.randperm(ct * ck, device=dev, generator=g).view(ct, ck),
+                        w=torch.rand(ct, ck, device=dev, generator=g), out=torch.empty(ct, ch, dtype=bf16, device=dev))
+
+        ops.append(Op(f"token_combine_k{ck}", f"moe_combine_bf16_T{ct}_k{ck}x{ch}", ct * ck * ch * 2 + ct * ch * 2 + ct * ck * 12,
+                      mkc, lambda b: native.token_combine_fwd(b["eo"], b["ui"], b["w"], b["out"]),
+                      ct * ck * ch * 2 + ct * ch * 2))
+    rt, re_, rk = 2048, 160, 6
+
+    def mkr():
+        return dict(lg=rn(rt, re_, dtype=torch.float32), w=torch.empty(rt, rk, device=dev),
+                    i=torch.empty(rt, rk, dtype=torch.int64, device=dev))
+
+    ops.append(Op("moe_router", "moe_router_f32_2048x160_top6", rt * re_ * 4 + rt * rk * 12, mkr,
+                  lambda b: native.moe_router_fwd(b["lg"], b["w"], b["i"], True), rt * re_ * 4))
     return ops
 
 

@@ -414,6 +414,110 @@ void swiglu_fp8_fwd(py::handle gate, py::handle up, py::handle y_fp8, py::handle
                                      st));
 }
 
+// ---- MoE dispatch (src/kernels/token_permute.rs, src/kernels/moe_router.rs) --
+
+View validate_int64_tensor(const char* name, const py::handle& obj) {
+  RawView r = validate_and_extract(name, obj);
+  if (r.dtype_str != "torch.int64") {
+    unsupported_dtype(std::string(name) + " must be int64, got " + r.dtype_str);
+  }
+  return View{r.ptr, -1, r.device_index, std::move(r.shape)};
+}
+
+// src/kernels/token_permute.rs:45-106. Calls the bounds-checked launcher (the
+// binding knows the source row count).
+void token_gather_fwd(py::handle src, py::handle indices, py::handle dst) {
+  View sv = validate_tensor("src", src);
+  View iv = validate_int64_tensor("indices", indices);
+  View dv = validate_tensor("dst", dst);
+  check_dtype_matches("dst", dv, sv, "x");
+  if (sv.shape.size() != 2 || dv.shape.size() != 2) {
+    shape_mismatch("src and dst must be 2-D; got src=" + shape_str(sv.shape) + ", dst=" + shape_str(dv.shape));
+  }
+  const int64_t hidden = sv.shape[1];
+  if (dv.shape[1] != hidden) {
+    shape_mismatch("dst's hidden dim (" + std::to_string(dv.shape[1]) + ") must match src's (" +
+                   std::to_string(hidden) + ")");
+  }
+  if (iv.shape.size() != 1 || iv.shape[0] != dv.shape[0]) {
+    shape_mismatch("indices shape " + shape_str(iv.shape) + " must be [" + std::to_string(dv.shape[0]) +
+                   "] (dst's row count)");
+  }
+  void* st = current_stream(sv.device_index);
+  check_launch("launch_token_gather_fwd",
+               launch_token_gather_checked_fwd((const void*)sv.ptr, (const int64_t*)iv.ptr, (void*)dv.ptr,
+                                               sv.shape[0], dv.shape[0], hidden, sv.dtype, st));
+}
+
+// src/kernels/token_permute.rs:115-201.
+void token_combine_fwd(py::handle expert_output, py::handle unpermute_index, py::handle weights,
+                       py::handle combined) {
+  View ev = validate_tensor("expert_output", expert_output);
+  View iv = validate_int64_tensor("unpermute_index", unpermute_index);
+  View wv = validate_tensor("weights", weights);
+  View cv = validate_tensor("combined", combined);
+  check_dtype_matches("combined", cv, ev, "x");
+  require_f32("weights", wv);
+  if (ev.shape.size() != 2 || cv.shape.size() != 2) {
+    shape_mismatch("expert_output and combined must be 2-D; got expert_output=" + shape_str(ev.shape) +
+                   ", combined=" + shape_str(cv.shape));
+  }
+  const int64_t hidden = ev.shape[1];
+  if (cv.shape[1] != hidden) {
+    shape_mismatch("combined's hidden dim (" + std::to_string(cv.shape[1]) + ") must match expert_output's (" +
+                   std::to_string(hidden) + ")");
+  }
+  if (iv.shape.size() != 2 || wv.shape.size() != 2) {
+    shape_mismatch("unpermute_index and weights must be 2-D [T, k]; got unpermute_index=" + shape_str(iv.shape) +
+                   ", weights=" + shape_str(wv.shape));
+  }
+  const int64_t n_tokens = iv.shape[0], k = iv.shape[1];
+  if (wv.shape != std::vector<int64_t>{n_tokens, k}) {
+    shape_mismatch("weights shape " + shape_str(wv.shape) + " must match unpermute_index's [" +
+                   std::to_string(n_tokens) + ", " + std::to_string(k) + "]");
+  }
+  if (cv.shape[0] != n_tokens) {
+    shape_mismatch("combined's row count (" + std::to_string(cv.shape[0]) + ") must match unpermute_index's [" +
+                   std::to_string(n_tokens) + ", ...]");
+  }
+  void* st = current_stream(ev.device_index);
+  check_launch("launch_token_combine_fwd",
+               launch_token_combine_checked_fwd((const void*)ev.ptr, (const int64_t*)iv.ptr, (const float*)wv.ptr,
+                                                (void*)cv.ptr, ev.shape[0], n_tokens, k, hidden, ev.dtype, st));
+}
+
+// src/kernels/moe_router.rs:36-116.
+void moe_router_fwd(py::handle logits, py::handle topk_weights, py::handle topk_indices, bool renormalize) {
+  View lv = validate_tensor("logits", logits);
+  View wv = validate_tensor("topk_weights", topk_weights);
+  View iv = validate_int64_tensor("topk_indices", topk_indices);
+  require_f32("topk_weights", wv);
+  if (lv.shape.size() != 2) {
+    shape_mismatch("logits must be 2-D [num_tokens, num_experts], got " + shape_str(lv.shape));
+  }
+  const int64_t n_tokens = lv.shape[0], n_experts = lv.shape[1];
+  if (wv.shape.size() != 2 || wv.shape[0] != n_tokens) {
+    shape_mismatch("topk_weights shape " + shape_str(wv.shape) + " must be [" + std::to_string(n_tokens) + ", k]");
+  }
+  const int64_t k = wv.shape[1];
+  if (iv.shape != std::vector<int64_t>{n_tokens, k}) {
+    shape_mismatch("topk_indices shape " + shape_str(iv.shape) + " must match topk_weights' [" +
+                   std::to_string(n_tokens) + ", " + std::to_string(k) + "]");
+  }
+  if (k > n_experts) {
+    throw std::runtime_error("k (" + std::to_string(k) + ") must be <= num_experts (" + std::to_string(n_experts) +
+                             ")");
+  }
+  if (n_experts > 256) {
+    shape_mismatch("num_experts (" + std::to_string(n_experts) +
+                   ") exceeds this kernel's supported maximum of 256");
+  }
+  void* st = current_stream(lv.device_index);
+  check_launch("launch_moe_router_fwd",
+               launch_moe_router_fwd((const void*)lv.ptr, (float*)wv.ptr, (int64_t*)iv.ptr, n_tokens, n_experts, k,
+                                     lv.dtype, renormalize ? 1 : 0, st));
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_native, m) {
@@ -434,6 +538,11 @@ PYBIND11_MODULE(_native, m) {
   m.def("rmsnorm_residual_fp8_fwd", &rmsnorm_residual_fp8_fwd, py::arg("x"), py::arg("residual"),
         py::arg("weight"), py::arg("y_fp8"), py::arg("scale"), py::arg("residual_out"), py::arg("eps"),
         py::arg("fp8_format"), py::arg("static_scale") = py::none());
+  m.def("token_gather_fwd", &token_gather_fwd, py::arg("src"), py::arg("indices"), py::arg("dst"));
+  m.def("token_combine_fwd", &token_combine_fwd, py::arg("expert_output"), py::arg("unpermute_index"),
+        py::arg("weights"), py::arg("combined"));
+  m.def("moe_router_fwd", &moe_router_fwd, py::arg("logits"), py::arg("topk_weights"), py::arg("topk_indices"),
+        py::arg("renormalize"));
   m.def("swiglu_fp8_fwd", &swiglu_fp8_fwd, py::arg("gate"), py::arg("up"), py::arg("y_fp8"), py::arg("scale"),
         py::arg("fp8_format"), py::arg("static_scale") = py::none());
 }

@@ -105,6 +105,49 @@ int32_t launch_swiglu_fp8_fwd(const void* gate, const void* up, uint8_t* y_fp8, 
                               int64_t rows, int64_t cols, float static_scale, int32_t scale_mode,
                               int32_t dtype, int32_t fp8_format, void* stream);
 
+/* ---- MoE dispatch path (the two memory-bound steps beside an FP8 MoE FFN). ---- */
+
+/* Row gather: dst[i] = src[indices[i]]. src: [S, hidden_dim], indices: int64
+ * [n_dst_rows], dst: [n_dst_rows, hidden_dim]; dtype F32/F16/BF16, or
+ * F8E4M3/F8E5M2 codes (the rows are moved as bytes; FP8 is an addition to
+ * the reference's three). A negative index yields a zero row; indices must be
+ * < S (this launcher is not told S, as in the reference).
+ * Replaces reference csrc/includes/token_permute.h:17-24. */
+int32_t launch_token_gather_fwd(const void* src, const int64_t* indices, void* dst, int64_t n_dst_rows,
+                                int64_t hidden_dim, int32_t dtype, void* stream);
+
+/* Weighted combine: combined[t] = sum_j weights[t,j] * expert_output[unpermute_index[t,j]],
+ * products rounded to fp32 and added in j order, the sum rounded to dtype.
+ * expert_output: [N, hidden_dim], unpermute_index: int64 [n_tokens, k], weights:
+ * float32 [n_tokens, k], combined: [n_tokens, hidden_dim]. A negative index
+ * drops its term.
+ * Replaces reference csrc/includes/token_permute.h:32-41. */
+int32_t launch_token_combine_fwd(const void* expert_output, const int64_t* unpermute_index,
+                                 const float* weights, void* combined, int64_t n_tokens, int64_t k,
+                                 int64_t hidden_dim, int32_t dtype, void* stream);
+
+/* As launch_token_gather_fwd / launch_token_combine_fwd, told the source row
+ * count: an index outside [0, n_src_rows) (resp. [0, n_expert_rows)) yields a
+ * zero row (resp. drops its term) instead of reading out of bounds. No
+ * reference counterpart; the Python binding calls these. */
+int32_t launch_token_gather_checked_fwd(const void* src, const int64_t* indices, void* dst,
+                                        int64_t n_src_rows, int64_t n_dst_rows, int64_t hidden_dim,
+                                        int32_t dtype, void* stream);
+int32_t launch_token_combine_checked_fwd(const void* expert_output, const int64_t* unpermute_index,
+                                         const float* weights, void* combined, int64_t n_expert_rows,
+                                         int64_t n_tokens, int64_t k, int64_t hidden_dim, int32_t dtype,
+                                         void* stream);
+
+/* Softmax top-k router: per token, probs = softmax(float(logits)); the k largest
+ * (descending; ties to the lower expert index) into topk_weights float32
+ * [num_tokens, k] and topk_indices int64 [num_tokens, k], renormalised to sum
+ * to 1 when renormalize != 0. num_experts <= 256 and k <= num_experts, else
+ * hipErrorInvalidValue.
+ * Replaces reference csrc/includes/moe_router.h:20-29. */
+int32_t launch_moe_router_fwd(const void* logits, float* topk_weights, int64_t* topk_indices,
+                              int64_t num_tokens, int64_t num_experts, int64_t k, int32_t dtype,
+                              int32_t renormalize, void* stream);
+
 /* ---- Diagnostics (no reference counterpart): device-side checks of the
  * arithmetic shortcuts used on the FP8 fast path. ---- */
 

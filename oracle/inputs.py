@@ -24,6 +24,15 @@ CONFIG_SHAPES = {
     "chain_rmsnorm": (16384, 4096),
     "chain_swiglu": (16384, 14336),
 }
+# MoE dispatch (the reference's standard cases, baselines/token_permute.py:128-146,
+# baselines/moe_router.py:72-79): gather 2048 -> 4096 rows of 4096; combine
+# T = 2048 at top-2 and top-6 over hidden 4096; router 2048 x 160 experts, top-6.
+MOE_SHAPES = {
+    "gather": (2048, 4096, 4096),      # (n_src_rows, n_dst_rows, hidden)
+    "combine_k2": (2048, 2, 4096),     # (n_tokens, k, hidden)
+    "combine_k6": (2048, 6, 4096),
+    "router": (2048, 160, 6),          # (n_tokens, n_experts, k)
+}
 ROPE_THETA = 500000.0
 RMS_EPS = 1e-5
 STATIC_SCALE = 0.05
@@ -83,3 +92,26 @@ def digest(*tensors: torch.Tensor) -> str:
     for t in tensors:
         h.update(t.contiguous().view(torch.uint8).numpy().tobytes() if t.numel() else b"")
     return h.hexdigest()[:16]
+
+
+def gather_inputs(n_src: int, n_dst: int, hidden: int, dtype=torch.bfloat16, seed: int = 0):
+    """src ~ N(0,1) [n_src, hidden]; indices uniform in [0, n_src), int64 [n_dst]."""
+    g = _gen(seed)
+    src = torch.randn((n_src, hidden), dtype=torch.float32, generator=g).to(dtype)
+    idx = torch.randint(0, max(n_src, 1), (n_dst,), generator=g, dtype=torch.int64) if n_src else \
+        torch.empty(n_dst, dtype=torch.int64)
+    return src, idx
+
+
+def combine_inputs(n_tokens: int, k: int, hidden: int, dtype=torch.bfloat16, seed: int = 0):
+    """expert_output ~ N(0,1) [T*k, hidden]; unpermute_index a random permutation
+    of range(T*k) as [T, k] (every expert row claimed once); weights U[0,1) fp32."""
+    g = _gen(seed)
+    eo = torch.randn((n_tokens * k, hidden), dtype=torch.float32, generator=g).to(dtype)
+    w = torch.rand((n_tokens, k), dtype=torch.float32, generator=g)
+    ui = torch.randperm(n_tokens * k, generator=g).reshape(n_tokens, k)
+    return eo, ui, w
+
+
+def router_inputs(n_tokens: int, n_experts: int, dtype=torch.float32, seed: int = 0) -> torch.Tensor:
+    return torch.randn((n_tokens, n_experts), dtype=torch.float32, generator=_gen(seed)).to(dtype)

@@ -20,6 +20,8 @@ _CTYPES = {
     "uint8_t*": ctypes.c_void_p,
     "float*": ctypes.c_void_p,
     "const float*": ctypes.c_void_p,
+    "const int64_t*": ctypes.c_void_p,
+    "int64_t*": ctypes.c_void_p,
     "int32_t*": ctypes.c_void_p,
     "unsigned long long*": ctypes.c_void_p,
     "int64_t": ctypes.c_int64,

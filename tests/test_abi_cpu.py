@@ -53,6 +53,14 @@ def test_empty_work_returns_success_without_device_calls():
     assert lib.launch_fp8_quant_static_fwd(None, None, 0.05, 0, 16, 2, 3, None) == 0
     assert lib.launch_rmsnorm_residual_fp8_fwd(None, None, None, None, None, None, 0, 16, 1e-5, 0.0, 0, 2, 3, None) == 0
     assert lib.launch_swiglu_fp8_fwd(None, None, None, None, 0, 16, 0.0, 0, 2, 3, None) == 0
+    assert lib.launch_token_gather_fwd(None, None, None, 0, 4096, 2, None) == 0
+    assert lib.launch_token_gather_fwd(None, None, None, 16, 0, 2, None) == 0
+    assert lib.launch_token_gather_checked_fwd(None, None, None, 8, 0, 4096, 2, None) == 0
+    assert lib.launch_token_combine_fwd(None, None, None, None, 0, 2, 4096, 2, None) == 0
+    assert lib.launch_token_combine_fwd(None, None, None, None, 16, 0, 4096, 2, None) == 0
+    assert lib.launch_token_combine_checked_fwd(None, None, None, None, 32, 16, 2, 0, 2, None) == 0
+    assert lib.launch_moe_router_fwd(None, None, None, 0, 16, 2, 0, 1, None) == 0
+    assert lib.launch_moe_router_fwd(None, None, None, 8, 16, 0, 0, 1, None) == 0
 
 
 def test_unknown_tags_return_invalid_value_before_device_calls():
@@ -68,6 +76,13 @@ def test_unknown_tags_return_invalid_value_before_device_calls():
     assert lib.launch_rmsnorm_residual_fp8_fwd(None, None, None, None, None, None, 4, 8, 1e-5, 0.0, 2, 2, 3, None) == 1
     assert lib.launch_swiglu_fp8_fwd(None, None, None, None, 4, 8, 0.0, 7, 2, 3, None) == 1
     assert lib.cck_fp8_cvt_selftest(0, 16, 1, None, None) == 1
+    assert lib.launch_token_gather_fwd(None, None, None, 4, 8, 7, None) == 1
+    assert lib.launch_token_gather_checked_fwd(None, None, None, -1, 4, 8, 2, None) == 1
+    assert lib.launch_token_combine_fwd(None, None, None, None, 4, 2, 8, 3, None) == 1  # fp8 is not a compute dtype
+    assert lib.launch_token_combine_checked_fwd(None, None, None, None, -1, 4, 2, 8, 2, None) == 1
+    assert lib.launch_moe_router_fwd(None, None, None, 4, 300, 2, 0, 1, None) == 1  # > 256 experts
+    assert lib.launch_moe_router_fwd(None, None, None, 4, 8, 9, 0, 1, None) == 1  # k > experts
+    assert lib.launch_moe_router_fwd(None, None, None, 4, 8, 2, 5, 1, None) == 1  # bad dtype
 
 
 class _Dev:
@@ -203,3 +218,37 @@ def test_python_api_argument_errors():
         kernels.fp8_quant(torch.randn(4, 8), "e4m3", "row")
     with pytest.raises(ValueError, match="static scale is per-tensor"):
         kernels.fp8_quant(torch.randn(4, 8), "e4m3", "token", scale=0.1)
+
+
+def test_token_permute_checks():
+    """src/kernels/token_permute.rs:45-201 validation branches, in order."""
+    i64 = torch.int64
+    _raises(native.token_gather_fwd, F(8, 16), F(4, dtype=torch.int32), F(4, 16), match="indices must be int64")
+    _raises(native.token_gather_fwd, F(8, 16), F(4, dtype=i64), F(4, 16, dtype=torch.float16), match="dtype mismatch")
+    _raises(native.token_gather_fwd, F(8, 16, 2), F(4, dtype=i64), F(4, 16), match="src and dst must be 2-D")
+    _raises(native.token_gather_fwd, F(8, 16), F(4, dtype=i64), F(4, 15), match="hidden dim")
+    _raises(native.token_gather_fwd, F(8, 16), F(5, dtype=i64), F(4, 16), match=r"indices shape \[5\] must be \[4\]")
+    _raises(native.token_gather_fwd, F(8, 16), F(4, 1, dtype=i64), F(4, 16), match="indices shape")
+    c = native.token_combine_fwd
+    _raises(c, F(8, 16), F(4, 2, dtype=i64), F(4, 2, dtype=torch.float16), F(4, 16), match="weights must be float32")
+    _raises(c, F(8, 16), F(4, 2, dtype=i64), F(4, 2, dtype=torch.float32), F(4, 16, dtype=torch.float32),
+            match="dtype mismatch")
+    _raises(c, F(8, 16, 1), F(4, 2, dtype=i64), F(4, 2, dtype=torch.float32), F(4, 16), match="must be 2-D")
+    _raises(c, F(8, 16), F(4, 2, dtype=i64), F(4, 2, dtype=torch.float32), F(4, 8), match="hidden dim")
+    _raises(c, F(8, 16), F(8, dtype=i64), F(4, 2, dtype=torch.float32), F(4, 16), match=r"must be 2-D \[T, k\]")
+    _raises(c, F(8, 16), F(4, 2, dtype=i64), F(4, 3, dtype=torch.float32), F(4, 16), match="weights shape")
+    _raises(c, F(8, 16), F(4, 2, dtype=i64), F(4, 2, dtype=torch.float32), F(5, 16), match="row count")
+
+
+def test_moe_router_checks():
+    """src/kernels/moe_router.rs:36-116 validation branches, in order."""
+    r = native.moe_router_fwd
+    i64 = torch.int64
+    _raises(r, F(4, 8), F(4, 2, dtype=torch.float16), F(4, 2, dtype=i64), True, match="topk_weights must be float32")
+    _raises(r, F(4, 8), F(4, 2, dtype=torch.float32), F(4, 2, dtype=torch.int32), True, match="must be int64")
+    _raises(r, F(4, 8, 1), F(4, 2, dtype=torch.float32), F(4, 2, dtype=i64), True, match="logits must be 2-D")
+    _raises(r, F(4, 8), F(3, 2, dtype=torch.float32), F(4, 2, dtype=i64), True, match=r"must be \[4, k\]")
+    _raises(r, F(4, 8), F(4, 2, dtype=torch.float32), F(4, 3, dtype=i64), True, match="topk_indices shape")
+    with pytest.raises(RuntimeError, match=r"k \(9\) must be <= num_experts \(8\)"):
+        r(F(4, 8), F(4, 9, dtype=torch.float32), F(4, 9, dtype=i64), True)
+    _raises(r, F(4, 300), F(4, 2, dtype=torch.float32), F(4, 2, dtype=i64), True, match="maximum of 256")

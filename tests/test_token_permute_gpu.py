@@ -1,0 +1,126 @@
+"""MoE token permute / unpermute kernels vs the CPU oracle (oracle/moe.py,
+restating baselines/token_permute.py:55-70, 215-217, 237-251).
+
+* gather is byte movement: bit-exact for every dtype (and FP8 rows);
+* combine: bit-exact where rows are a multiple of 16 elements (the oracle's
+  torch sum then adds in j order, as the kernel does); elsewhere within one
+  storage ulp (tests/_parity.py ULP_TOL); fp32 always within 1e-6 relative;
+* the reference's case tables (baselines/token_permute.py:128-167) in three
+  dtypes, its vector-tail sweep (tests/test_token_permute_kernel.py:107-137),
+  the permute -> unpermute round trip, and index hygiene (out-of-range
+  indices give zero rows / dropped terms).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from custom_cuda_kernals_amd.kernels import compute_permutation, token_combine, token_gather
+from oracle import inputs, moe
+from tests._parity import assert_ulp_close, bits_equal
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+GATHER_CASES = [(2048, 4096, 4096), (2048, 4096, 11008), (257, 513, 100), (1, 1, 256), (64, 0, 256),
+                (128, 256, 16)]
+COMBINE_CASES = [(2048, 2, 4096), (2048, 6, 4096), (256, 1, 512), (256, 8, 512), (257, 3, 100), (1, 2, 256),
+                 (0, 2, 256), (128, 4, 16)]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", GATHER_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_gather_matches_oracle(case, dtype):
+    s, n, h = case
+    src, idx = inputs.gather_inputs(s, n, h, dtype, seed=s + n + h)
+    out = token_gather(src.cuda(), idx.cuda()).cpu()
+    assert out.shape == (n, h) and out.dtype == dtype
+    assert bits_equal(out, moe.token_gather(src, idx)).all()
+
+
+@pytest.mark.parametrize("fmt", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("h", [4096, 100, 7])
+def test_gather_fp8_rows(fmt, h):
+    src = torch.randint(0, 256, (300, h), dtype=torch.uint8).view(fmt)
+    idx = torch.randint(0, 300, (777,))
+    out = token_gather(src.cuda(), idx.cuda()).cpu()
+    assert torch.equal(out.view(torch.uint8), src.view(torch.uint8)[idx])
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_gather_vector_tails(dtype):
+    for h in list(range(1, 40)) + [63, 64, 65, 127, 128, 129]:
+        src, idx = inputs.gather_inputs(33, 45, h, dtype, seed=h)
+        out = token_gather(src.cuda(), idx.cuda()).cpu()
+        assert bits_equal(out, moe.token_gather(src, idx)).all(), h
+
+
+def test_gather_out_of_range_rows_are_zero():
+    src, idx = inputs.gather_inputs(50, 64, 256, torch.bfloat16, seed=1)
+    idx[3], idx[10], idx[40] = 50, -1, 1 << 40
+    out = token_gather(src.cuda(), idx.cuda()).cpu()
+    bad = torch.tensor([3, 10, 40])
+    assert torch.equal(out[bad], torch.zeros(3, 256, dtype=torch.bfloat16))
+    good = torch.ones(64, dtype=torch.bool)
+    good[bad] = False
+    assert bits_equal(out[good], src[idx[good]]).all()
+
+
+def _check_combine(eo, ui, w):
+    out = token_combine(eo.cuda(), ui.cuda(), w.cuda()).cpu()
+    ref = moe.token_combine(eo, ui, w)
+    assert out.shape == ref.shape and out.dtype == eo.dtype
+    if out.numel() == 0:
+        return None
+    if eo.shape[1] % 16 == 0:
+        assert bits_equal(out, ref).all()
+        assert bits_equal(out, moe.combine_sequential(eo, ui, w)).all()
+        return 1.0
+    if eo.dtype == torch.float32:
+        torch.testing.assert_close(out, ref, rtol=1e-6, atol=1e-6)
+        return None
+    return assert_ulp_close(out, ref, "combine")["bit_exact_fraction"]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", COMBINE_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_combine_matches_oracle(case, dtype):
+    t, k, h = case
+    eo, ui, w = inputs.combine_inputs(t, k, h, dtype, seed=t + k + h)
+    _check_combine(eo, ui, w)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_combine_vector_tails(dtype):
+    for h in list(range(1, 20)) + [31, 32, 33, 127, 128, 129]:
+        eo, ui, w = inputs.combine_inputs(17, 3, h, dtype, seed=h)
+        _check_combine(eo, ui, w)
+
+
+def test_combine_out_of_range_terms_are_dropped():
+    eo, ui, w = inputs.combine_inputs(64, 4, 256, torch.bfloat16, seed=2)
+    ui[5, 1], ui[9, 0], ui[9, 3] = 256, -7, 1 << 40
+    out = token_combine(eo.cuda(), ui.cuda(), w.cuda()).cpu()
+    w_ref, ui_ref = w.clone(), ui.clone()
+    for t, j in ((5, 1), (9, 0), (9, 3)):
+        w_ref[t, j], ui_ref[t, j] = 0.0, 0
+    assert bits_equal(out, moe.token_combine(eo, ui_ref, w_ref)).all()
+
+
+def test_dispatch_round_trip():
+    """Router assignments -> compute_permutation -> gather -> (identity experts)
+    -> combine with the renormalised weights gives back the tokens: the MoE
+    dispatch path of the reference (tests/test_token_permute_kernel.py:89-104)."""
+    t, k, e, h = 512, 2, 8, 1024
+    g = torch.Generator().manual_seed(4)
+    hidden = torch.randn(t, h, generator=g)
+    topk = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(t)])
+    perm, unperm = compute_permutation(topk.cuda())
+    p_ref, u_ref = moe.compute_permutation(topk.numpy())
+    assert np.array_equal(perm.cpu().numpy(), p_ref) and np.array_equal(unperm.cpu().numpy(), u_ref)
+    permuted = token_gather(hidden.cuda(), perm)
+    w = torch.full((t, k), 1.0 / k)
+    back = token_combine(permuted, unperm, w.cuda()).cpu()
+    torch.testing.assert_close(back, hidden, rtol=1e-6, atol=1e-6)
