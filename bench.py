@@ -65,9 +65,10 @@ def _ensure_built():
 class Op:
     """One benchmarked op: a buffer-set factory, a launch on set i, algorithmic bytes."""
 
-    def __init__(self, name, workload, nbytes, make_set, launch, set_bytes):
+    def __init__(self, name, workload, nbytes, make_set, launch, set_bytes, shape=None):
         self.name, self.workload, self.nbytes = name, workload, nbytes
         self.make_set, self.launch, self.set_bytes = make_set, launch, set_bytes
+        self.shape = shape
 
 
 def _ops(torch, native):
@@ -91,7 +92,7 @@ def _ops(torch, native):
         return dict(x=x, q=torch.empty(m1, n1, dtype=f8, device=dev), s=torch.empty(m1, device=dev))
 
     ops.append(Op("fp8_quant_token", "fp8_token_bf16_2048x4096", m1 * n1 * 3 + m1 * 4, mk1,
-                  lambda b: native.fp8_quant_token_fwd(b["x"], b["q"], b["s"], "e4m3"), m1 * n1 * 3))
+                  lambda b: native.fp8_quant_token_fwd(b["x"], b["q"], b["s"], "e4m3"), m1 * n1 * 3, [m1, n1]))
 
     # 2: RMSNorm + residual, [8192, 4096] bf16, eps 1e-5
     m2, n2 = 8192, 4096
@@ -102,7 +103,8 @@ def _ops(torch, native):
                     ro=torch.empty(m2, n2, dtype=bf16, device=dev))
 
     ops.append(Op("rmsnorm_residual", "rmsnorm_residual_bf16_8192x4096", m2 * n2 * 8 + n2 * 2, mk2,
-                  lambda b: native.rmsnorm_residual_fwd(b["x"], b["r"], w2, b["y"], b["ro"], 1e-5), m2 * n2 * 8))
+                  lambda b: native.rmsnorm_residual_fwd(b["x"], b["r"], w2, b["y"], b["ro"], 1e-5), m2 * n2 * 8,
+                  [m2, n2]))
 
     # 3 / 3v: SwiGLU [8192, 14336] bf16, and SwiGLU + per-token FP8
     m3, n3 = 8192, 14336
@@ -112,9 +114,10 @@ def _ops(torch, native):
                     q=torch.empty(m3, n3, dtype=f8, device=dev), s=torch.empty(m3, device=dev))
 
     ops.append(Op("swiglu", "swiglu_bf16_8192x14336", m3 * n3 * 6, mk3,
-                  lambda b: native.swiglu_fwd(b["g"], b["u"], b["y"]), m3 * n3 * 6))
+                  lambda b: native.swiglu_fwd(b["g"], b["u"], b["y"]), m3 * n3 * 6, [m3, n3]))
     ops.append(Op("swiglu_fp8_token", "swiglu_fp8_token_bf16_8192x14336", m3 * n3 * 5 + m3 * 4, mk3,
-                  lambda b: native.swiglu_fp8_fwd(b["g"], b["u"], b["q"], b["s"], "e4m3", None), m3 * n3 * 5))
+                  lambda b: native.swiglu_fp8_fwd(b["g"], b["u"], b["q"], b["s"], "e4m3", None), m3 * n3 * 5,
+                  [m3, n3]))
 
     # 4: RoPE in place, q [8,4096,32,128], k [8,4096,8,128] bf16, theta 5e5
     B, S, HQ, HKV, D = 8, 4096, 32, 8, 128
@@ -127,7 +130,8 @@ def _ops(torch, native):
         return dict(q=rn(B, S, HQ, D), k=rn(B, S, HKV, D))
 
     ops.append(Op("rope_inplace", "rope_bf16_q8x4096x32x128_k8x4096x8x128", rope_elems * 4 + 2 * S * (D // 2) * 4, mk4,
-                  lambda b: native.rope_fwd(b["q"], b["k"], cos4, sin4, b["q"], b["k"]), rope_elems * 4))
+                  lambda b: native.rope_fwd(b["q"], b["k"], cos4, sin4, b["q"], b["k"]), rope_elems * 4,
+                  [B, S, HQ, HKV, D]))
 
     # 5a / 5b: T = 16384 chain, per-token and static 0.05
     m5, n5a, n5b = 16384, 4096, 14336
@@ -205,7 +209,7 @@ def _time_op(torch, op, steps, warmup, use_graph=True):
         us = ms * 1000.0 / steps
         del sets
         torch.cuda.empty_cache()
-        return {"workload": op.workload, "us": round(us, 3),
+        return {"workload": op.workload, "shape": op.shape, "us": round(us, 3),
                 "GB_per_s": round(op.nbytes / (us * 1e-6) / 1e9, 1), "steps": steps, "graph": False}
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
@@ -229,7 +233,7 @@ def _time_op(torch, op, steps, warmup, use_graph=True):
     gbps = op.nbytes / (us * 1e-6) / 1e9
     del graph, sets
     torch.cuda.empty_cache()
-    return {"workload": op.workload, "us": round(us, 3), "GB_per_s": round(gbps, 1),
+    return {"workload": op.workload, "shape": op.shape, "us": round(us, 3), "GB_per_s": round(gbps, 1),
             "frac_of_8TBps": round(gbps / PEAK_GBPS, 4), "algorithmic_bytes": op.nbytes,
             "steps": steps, "buffer_sets": nsets, "total_ms": round(ms, 4)}
 
@@ -349,7 +353,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) inputs generated on the GPU, resident in HBM)",
-        "config": {"workload": head["workload"], "op": head_name, "global_batch": 8192, "seq_len": 1,
+        "config": {"workload": head["workload"], "op": head_name, "shape": head.get("shape"),
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBPS, 4), "traffic": _traffic(head_name)},

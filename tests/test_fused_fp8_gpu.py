@@ -126,3 +126,13 @@ def test_every_bf16_gate_fused_table_rows():
     u = torch.randn(16, 16384, generator=gen).to(torch.bfloat16)
     for static in (None, 0.05):
         _check_swiglu(g, u, "e4m3", static)
+
+
+@pytest.mark.parametrize("static", [None, 0.05])
+@pytest.mark.parametrize("shape", [(77, 14336), (9, 20008), (130, 8200)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_swiglu_fp8_table_paths_ragged(shape, static):
+    """bf16 shapes on the LDS-table kernels with partial tiles: rows of
+    1024 x 2 and 1024 x 4 vectors (per-token) and a static stream whose length
+    is not a multiple of the 16384-element tile."""
+    g, u = inputs.swiglu_inputs(*shape, torch.bfloat16, seed=shape[1])
+    _check_swiglu(g, u, "e4m3", static)
