@@ -127,18 +127,41 @@ struct SiluTableBF16 {
   static constexpr uint32_t kLo = 0x3880;                    // 2^-14
   static constexpr uint32_t kHi = 0x4200;                    // 32.0
   static constexpr uint32_t kEntries = 2 * (kHi - kLo);      // 4864
-  static constexpr uint32_t kTinyKeys = 2 * (0x3b00 - kLo);  // |g| < 2^-9
 
-  // Rounded SiLU of every tabulated value. For |g| < 2^-9, sigmoid(g) =
-  // 1/2 + g/4 + O(g^3), so g*sigmoid(g) = (g/2)(1 + d) with |d| < 2^-10,
-  // inside half a bf16 ulp of the exactly representable g/2: those entries
-  // are g/2 without evaluating the SiLU (keys below kTinyKeys, a
-  // wave-uniform branch).
+  // Rounded SiLU of every tabulated value, filled as (+a, -a) pairs: the
+  // keys of +a and -a are adjacent (2p, 2p + 1 for magnitude field kLo + p).
+  // * |g| < 2^-9: sigmoid(g) = 1/2 + g/4 + O(g^3), so g*sigmoid(g) = (g/2)(1 + d)
+  //   with |d| < 2^-10, inside half a bf16 ulp of the exactly representable g/2:
+  //   those entries are +-a/2 without evaluating the SiLU (pairs below
+  //   kTinyPairs, a wave-uniform branch).
+  // * a <= kFastAbs: e = exp(-a) and r = 1/(1+e) serve both signs, since
+  //   sigmoid(-a) = e * r: silu(+a) = a*r, silu(-a) = -a*(e*r). Rounded to bf16
+  //   this equals silu_one on both signs for every bf16 magnitude in range
+  //   (checked exhaustively on the device: the table kernels equal the
+  //   arithmetic kernels for all 2^16 gates), at one exp and one reciprocal
+  //   per pair instead of per entry.
+  // * larger a: silu(+a) = a exactly (exp(-a) < 2^-25, so 1 + exp(-a) rounds to
+  //   1 in silu_exact), and silu_one(-a) for the negative sign.
+  static constexpr uint32_t kPairs = kHi - kLo;
+  static constexpr uint32_t kTinyPairs = 0x3b00 - kLo;  // a < 2^-9
   __device__ static void fill(float* tab, int tid, int nthreads) {
-    for (uint32_t i = tid; i < kEntries; i += nthreads) {
-      const uint32_t key = i + 2 * kLo;
-      const float g = bits_f32((((key & 1u) << 15) | (key >> 1)) << 16);
-      tab[i] = i < kTinyKeys ? g * 0.5f : CodecBF16::round(silu_one<CodecBF16>(g));
+    using K = SiluConsts<CodecBF16>;
+    for (uint32_t p = tid; p < kPairs; p += nthreads) {
+      const float a = bits_f32((kLo + p) << 16);
+      float pos, neg;
+      if (p < kTinyPairs) {
+        pos = a * 0.5f;
+        neg = -a * 0.5f;
+      } else if (a <= K::kFastAbs) {
+        const float e = exp_neg_fast<CodecBF16>(a);
+        const float r = recip_refined(1.0f + e);
+        pos = CodecBF16::round(a * r);
+        neg = CodecBF16::round(-a * (e * r));
+      } else {
+        pos = a;
+        neg = CodecBF16::round(silu_one<CodecBF16>(-a));
+      }
+      *reinterpret_cast<f32x2*>(tab + 2 * p) = (f32x2){pos, neg};
     }
   }
 
@@ -196,7 +219,7 @@ template <class C, int THREADS, int UNROLL, bool TAB>
 __global__ __launch_bounds__(THREADS) void swiglu_flat(const u32x4* __restrict__ gate,
                                                        const u32x4* __restrict__ up,
                                                        u32x4* __restrict__ y, int64_t nvec) {
-  __shared__ float tab[TAB ? SiluTableBF16::kEntries : 1];
+  __shared__ __attribute__((aligned(16))) float tab[TAB ? SiluTableBF16::kEntries : 1];
   const int64_t stride = (int64_t)gridDim.x * THREADS * UNROLL;
   int64_t base = (int64_t)blockIdx.x * THREADS * UNROLL + threadIdx.x;
   u32x4 g[UNROLL], u[UNROLL];
@@ -256,7 +279,7 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_static_flat(const u32x4* _
                                                                  uint8_t* __restrict__ yq, float s,
                                                                  int64_t nvec) {
   constexpr int VEC = C::VEC;
-  __shared__ float tab[TAB ? SiluTableBF16::kEntries : 1];
+  __shared__ __attribute__((aligned(16))) float tab[TAB ? SiluTableBF16::kEntries : 1];
   const float r = 1.0f / s;
   const bool scale_ok = fast_path_ok<FMT>(s, r, 0.0f);
   const int64_t stride = (int64_t)gridDim.x * THREADS * UNROLL;
@@ -336,7 +359,7 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
   constexpr int NW = THREADS / 64;
   constexpr int VEC = C::VEC;
   __shared__ uint32_t lds[2 * NW];
-  __shared__ float tab[TAB ? SiluTableBF16::kEntries : 1];
+  __shared__ __attribute__((aligned(16))) float tab[TAB ? SiluTableBF16::kEntries : 1];
   const int nvec = (int)(cols / VEC);
   int parity = 0;
   // Global-pointer row access: for this kernel's 1024 x 2 shape it measured
