@@ -69,19 +69,6 @@ inline unsigned row_grid(int64_t rows) {
   return (unsigned)(rows < cap ? rows : cap);
 }
 
-// Compute units of the current device (cached per device ordinal).
-inline int cu_count() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
-
 inline unsigned flat_grid(int64_t work_items, int threads, int64_t cap) {
   int64_t g = (work_items + threads - 1) / threads;
   if (g < 1) g = 1;
