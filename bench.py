@@ -10,6 +10,10 @@ input/output buffers, rotating over enough sets that the working set is
 >= 2 GiB, so no step can be served from the 256 MB Infinity Cache left warm by
 the previous one.
 
+Each op also reports "per_call": the reference's own methodology (a cache
+flush before every call, HIP events around one call through the binding, so
+validation and launch latency are inside the window), as median and IQR.
+
 The headline `value` is the BASELINE config-2 workload (fused RMSNorm +
 residual, bf16 [8192, 4096]); every other config's op is reported under "ops".
 Achieved bandwidth = algorithmic bytes per launch / average launch duration.
@@ -149,15 +153,15 @@ def _ops(torch, native):
     ops.append(Op("rmsnorm_residual_fp8_token", "chain_rmsnorm_fp8_token_bf16_16384x4096",
                   e5a * 7 + m5 * 4 + n5a * 2, mk5a,
                   lambda b: native.rmsnorm_residual_fp8_fwd(b["x"], b["r"], w5, b["q"], b["s"], b["ro"], 1e-5, "e4m3", None),
-                  e5a * 7))
+                  e5a * 7, [m5, n5a]))
     ops.append(Op("swiglu_fp8_token_T16384", "chain_swiglu_fp8_token_bf16_16384x14336", e5b * 5 + m5 * 4, mk5b,
-                  lambda b: native.swiglu_fp8_fwd(b["g"], b["u"], b["q"], b["s"], "e4m3", None), e5b * 5))
+                  lambda b: native.swiglu_fp8_fwd(b["g"], b["u"], b["q"], b["s"], "e4m3", None), e5b * 5, [m5, n5b]))
     ops.append(Op("rmsnorm_residual_fp8_static", "chain_rmsnorm_fp8_static0.05_bf16_16384x4096",
                   e5a * 7 + n5a * 2, mk5a,
                   lambda b: native.rmsnorm_residual_fp8_fwd(b["x"], b["r"], w5, b["q"], None, b["ro"], 1e-5, "e4m3", 0.05),
-                  e5a * 7))
+                  e5a * 7, [m5, n5a]))
     ops.append(Op("swiglu_fp8_static_T16384", "chain_swiglu_fp8_static0.05_bf16_16384x14336", e5b * 5, mk5b,
-                  lambda b: native.swiglu_fp8_fwd(b["g"], b["u"], b["q"], None, "e4m3", 0.05), e5b * 5))
+                  lambda b: native.swiglu_fp8_fwd(b["g"], b["u"], b["q"], None, "e4m3", 0.05), e5b * 5, [m5, n5b]))
 
     # MoE dispatch (the reference's standard cases, baselines/token_permute.py:128-146 and
     # baselines/moe_router.py:72-79): not BASELINE configs; reported beside them.
@@ -168,7 +172,8 @@ def _ops(torch, native):
                     dst=torch.empty(gd, gh, dtype=bf16, device=dev))
 
     ops.append(Op("token_gather", "moe_gather_bf16_2048to4096x4096", gd * gh * 4 + gd * 8, mkg,
-                  lambda b: native.token_gather_fwd(b["src"], b["idx"], b["dst"]), gs * gh * 2 + gd * gh * 2))
+                  lambda b: native.token_gather_fwd(b["src"], b["idx"], b["dst"]), gs * gh * 2 + gd * gh * 2,
+                  [gs, gd, gh]))
     for ck in (2, 6):
         ct, ch = 2048, 4096
 
@@ -178,7 +183,7 @@ def _ops(torch, native):
 
         ops.append(Op(f"token_combine_k{ck}", f"moe_combine_bf16_T{ct}_k{ck}x{ch}", ct * ck * ch * 2 + ct * ch * 2 + ct * ck * 12,
                       mkc, lambda b: native.token_combine_fwd(b["eo"], b["ui"], b["w"], b["out"]),
-                      ct * ck * ch * 2 + ct * ch * 2))
+                      ct * ck * ch * 2 + ct * ch * 2, [ct, ck, ch]))
     rt, re_, rk = 2048, 160, 6
 
     def mkr():
@@ -186,7 +191,7 @@ def _ops(torch, native):
                     i=torch.empty(rt, rk, dtype=torch.int64, device=dev))
 
     ops.append(Op("moe_router", "moe_router_f32_2048x160_top6", rt * re_ * 4 + rt * rk * 12, mkr,
-                  lambda b: native.moe_router_fwd(b["lg"], b["w"], b["i"], True), rt * re_ * 4))
+                  lambda b: native.moe_router_fwd(b["lg"], b["w"], b["i"], True), rt * re_ * 4, [rt, re_, rk]))
     return ops
 
 
@@ -231,11 +236,35 @@ def _time_op(torch, op, steps, warmup, use_graph=True):
     ms = start.elapsed_time(end)
     us = ms * 1000.0 / steps
     gbps = op.nbytes / (us * 1e-6) / 1e9
-    del graph, sets
+    del graph
+    per_call = _per_call_us(torch, op, sets)
+    del sets
     torch.cuda.empty_cache()
     return {"workload": op.workload, "shape": op.shape, "us": round(us, 3), "GB_per_s": round(gbps, 1),
             "frac_of_8TBps": round(gbps / PEAK_GBPS, 4), "algorithmic_bytes": op.nbytes,
-            "steps": steps, "buffer_sets": nsets, "total_ms": round(ms, 4)}
+            "steps": steps, "buffer_sets": nsets, "total_ms": round(ms, 4), "per_call": per_call}
+
+
+def _per_call_us(torch, op, sets, calls=30):
+    """The reference's methodology (benchmarks/*_bench.py, examples/llama_block.py:220-250):
+    a 512 MiB write between calls so nothing is cache-resident, then HIP events
+    around one call through the binding (validation and launch included);
+    median and inter-quartile range in microseconds."""
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    times = []
+    for i in range(calls):
+        flush.fill_(i & 0xFF)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        op.launch(sets[i % len(sets)])
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) * 1000.0)
+    del flush
+    times.sort()
+    q = lambda f: times[min(len(times) - 1, int(f * len(times)))]
+    return {"median_us": round(q(0.5), 3), "iqr_us": round(q(0.75) - q(0.25), 3), "calls": calls}
 
 
 def _cpu_baseline(budget_s: float):
