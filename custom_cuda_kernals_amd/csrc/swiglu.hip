@@ -367,14 +367,14 @@ __global__ __launch_bounds__(256) void swiglu_fp8_static_scalar(const void* __re
   }
 }
 
-// FP8 variant, register-resident rows; y is kept as floats (already rounded
-// to T) between the amax reduction and the quantisation. STATIC selects the
-// static scale; TAB (bf16) the LDS SiLU table, filled while the first row's
-// loads are in flight.
-template <class C, int THREADS, int ITEMS, bool STATIC, int FMT, bool TAB>
+// Per-token FP8 variant, register-resident rows; y is kept as floats (already
+// rounded to T) between the amax reduction and the quantisation. TAB (bf16)
+// selects the LDS SiLU table, filled while the first row's loads are in
+// flight. (A static scale needs no row reduction: swiglu_fp8_static_flat.)
+template <class C, int THREADS, int ITEMS, int FMT, bool TAB>
 __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
     const void* __restrict__ gate, const void* __restrict__ up, uint8_t* __restrict__ yq,
-    float* __restrict__ scale, int64_t rows, int64_t cols, float static_scale) {
+    float* __restrict__ scale, int64_t rows, int64_t cols) {
   constexpr int NW = THREADS / 64;
   constexpr int VEC = C::VEC;
   __shared__ uint32_t lds[2 * NW];
@@ -428,13 +428,8 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
     // amax >= 0 (or NaN), so unsigned max on its bits is the float maximum.
     amax = bits_f32(block_allreduce<NW>(f32_bits(amax), MaxU32{}, lds, parity));
     parity ^= 1;
-    float s;
-    if constexpr (STATIC) {
-      s = static_scale;
-    } else {
-      s = scale_from_amax<FMT>(amax);
-      if (threadIdx.x == 0) scale[row] = s;
-    }
+    const float s = scale_from_amax<FMT>(amax);
+    if (threadIdx.x == 0) scale[row] = s;
     const float r = 1.0f / s;
     const bool fast = fast_path_ok<FMT>(s, r, amax);
     const RowBuf<false> bq(yq + row * cols, (uint32_t)cols);
@@ -459,11 +454,12 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
   }
 }
 
-// FP8 variant, any alignment / row length: y is recomputed in the second pass.
-template <class C, bool STATIC, int FMT>
+// Per-token FP8 variant, any alignment / row length: y is recomputed in the
+// second pass.
+template <class C, int FMT>
 __global__ __launch_bounds__(256) void swiglu_fp8_generic(
     const void* __restrict__ gate, const void* __restrict__ up, uint8_t* __restrict__ yq,
-    float* __restrict__ scale, int64_t rows, int64_t cols, float static_scale) {
+    float* __restrict__ scale, int64_t rows, int64_t cols) {
   __shared__ uint32_t lds[2 * 4];
   int parity = 0;
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
@@ -475,13 +471,8 @@ __global__ __launch_bounds__(256) void swiglu_fp8_generic(
     }
     amax = bits_f32(block_allreduce<4>(f32_bits(amax), MaxF32{}, lds, parity));
     parity ^= 1;
-    float s;
-    if constexpr (STATIC) {
-      s = static_scale;
-    } else {
-      s = scale_from_amax<FMT>(amax);
-      if (threadIdx.x == 0) scale[row] = s;
-    }
+    const float s = scale_from_amax<FMT>(amax);
+    if (threadIdx.x == 0) scale[row] = s;
     const float r = 1.0f / s;
     const bool fast = fast_path_ok<FMT>(s, r, amax);
     for (int64_t j = threadIdx.x; j < cols; j += 256) {
@@ -492,9 +483,9 @@ __global__ __launch_bounds__(256) void swiglu_fp8_generic(
   }
 }
 
-template <class C, bool STATIC, int FMT>
-int32_t launch_swiglu_fp8(const void* gate, const void* up, uint8_t* yq, float* scale, int64_t rows,
-                          int64_t cols, float static_scale, hipStream_t st) {
+template <class C, int FMT>
+int32_t launch_swiglu_fp8_token(const void* gate, const void* up, uint8_t* yq, float* scale, int64_t rows,
+                                int64_t cols, hipStream_t st) {
   const bool vec_ok = (cols % C::VEC == 0) && host_aligned(gate, 16) && host_aligned(up, 16) &&
                       host_aligned(yq, C::VEC);
   const int64_t nvec = cols / C::VEC;
@@ -503,15 +494,15 @@ int32_t launch_swiglu_fp8(const void* gate, const void* up, uint8_t* yq, float* 
     using S = decltype(shape);
     // The table pays for its per-workgroup fill only on long rows.
     constexpr bool kTab = std::is_same_v<C, CodecBF16> && S::kThreads == 1024;
-    swiglu_fp8_resident<C, S::kThreads, S::kItems, STATIC, FMT, kTab><<<g, S::kThreads, 0, st>>>(
-        gate, up, yq, scale, rows, cols, static_scale);
+    swiglu_fp8_resident<C, S::kThreads, S::kItems, FMT, kTab><<<g, S::kThreads, 0, st>>>(gate, up, yq, scale,
+                                                                                          rows, cols);
   };
   // At most two vectors per thread keeps the kernel under 64 VGPRs of row
   // state; 1024-thread rows measured fastest on MI355X at cols = 14336 bf16.
   const bool done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
                                              RowShape<512, 2>, RowShape<1024, 2>, RowShape<1024, 4>>(nvec, run);
   if (!done) {
-    swiglu_fp8_generic<C, STATIC, FMT><<<g, 256, 0, st>>>(gate, up, yq, scale, rows, cols, static_scale);
+    swiglu_fp8_generic<C, FMT><<<g, 256, 0, st>>>(gate, up, yq, scale, rows, cols);
   }
   return launch_status();
 }
@@ -574,7 +565,7 @@ extern "C" int32_t launch_swiglu_fp8_fwd(const void* gate, const void* up, uint8
     using C = decltype(codec);
     return with_fp8(fp8_format, [&](auto f) {
       constexpr int FMT = decltype(f)::value;
-      if (scale_mode == 0) return launch_swiglu_fp8<C, false, FMT>(gate, up, y_fp8, scale, rows, cols, 0.0f, st);
+      if (scale_mode == 0) return launch_swiglu_fp8_token<C, FMT>(gate, up, y_fp8, scale, rows, cols, st);
       // Static scale: one flat stream over rows * cols elements.
       const int64_t n = rows * cols;
       int64_t done = 0;
