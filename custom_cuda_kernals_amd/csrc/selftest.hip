@@ -8,8 +8,13 @@
 //   cck_div_selftest      - div_by_scale (three-op division) against IEEE
 //                           division x / s for caller-given x and s sets;
 //   cck_scale_selftest    - scale_from_amax (fma-corrected / 7) against
-//                           clamp(amax / FP8_MAX, 1e-12) with IEEE division.
+//                           clamp(amax / FP8_MAX, 1e-12) with IEEE division;
+//   cck_silu_table_selftest - both fills of the bf16 SiLU table against the
+//                           arithmetic SiLU entry by entry, and the table
+//                           lookup against the arithmetic path for all 2^16
+//                           bf16 gates.
 #include "launch.hpp"
+#include "silu.hpp"
 
 namespace cck {
 namespace {
@@ -105,6 +110,71 @@ __global__ __launch_bounds__(256) void scale_selftest(uint64_t start, uint64_t c
   }
 }
 
+// counters (unsigned long long[6]):
+//   [0] fill_single entries that differ (bitwise) from CodecBF16::round(silu_one(g))
+//   [1] fill_pairs entries that differ likewise
+//   [2] lowest table index counted in [0] or [1] (init ~0)
+//   [3] gates whose silu_vec<CodecBF16, true> (table of fill_pairs) differs
+//       bitwise from silu_vec<CodecBF16, false>, over all 2^16 bf16 patterns in
+//       two groupings into 8-gate vectors: ascending, and permuted by an odd
+//       multiplier mod 2^16 (mixes in-range and out-of-range gates)
+//   [4] vectors of [3] served by the table (all 8 gates in range)
+//   [5] gates checked in [3] (2^17)
+// One workgroup of 1024 threads.
+__global__ __launch_bounds__(1024) void silu_table_selftest(unsigned long long* counters) {
+  using T = SiluTableBF16;
+  __shared__ __attribute__((aligned(16))) float tab[T::kEntries];
+  unsigned long long bad[2] = {0, 0}, lo = ~0ull;
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    if (f == 0) {
+      T::fill_single(tab, threadIdx.x, 1024);
+    } else {
+      T::fill_pairs(tab, threadIdx.x, 1024);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < T::kEntries; i += 1024) {
+      const uint32_t key = i + 2 * T::kLo;
+      const float g = bits_f32((((key & 1u) << 15) | (key >> 1)) << 16);
+      const float want = CodecBF16::round(silu_one<CodecBF16>(g));
+      if (f32_bits(tab[i]) != f32_bits(want)) {
+        bad[f] += 1;
+        lo = lo < i ? lo : i;
+      }
+    }
+    __syncthreads();
+  }
+  constexpr uint32_t kVecs = 65536 / 8;
+  unsigned long long diff = 0, hits = 0, checked = 0;
+  for (uint32_t v = threadIdx.x; v < 2 * kVecs; v += 1024) {
+    const bool permuted = v >= kVecs;
+    const uint32_t first = (v % kVecs) * 8;
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t p0 = first + 2 * j, p1 = p0 + 1;
+      if (permuted) {
+        p0 = (p0 * 40503u) & 0xffffu;
+        p1 = (p1 * 40503u) & 0xffffu;
+      }
+      w[j] = p0 | (p1 << 16);
+    }
+    float a[8], b[8], t[8];
+    silu_vec<CodecBF16, true>(w, tab, a);
+    silu_vec<CodecBF16, false>(w, nullptr, b);
+    hits += T::lookup8(w, tab, t) ? 1 : 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) diff += f32_bits(a[i]) != f32_bits(b[i]);
+    checked += 8;
+  }
+  if (bad[0]) atomicAdd(&counters[0], bad[0]);
+  if (bad[1]) atomicAdd(&counters[1], bad[1]);
+  if (lo != ~0ull) atomicMin(&counters[2], lo);
+  if (diff) atomicAdd(&counters[3], diff);
+  if (hits) atomicAdd(&counters[4], hits);
+  if (checked) atomicAdd(&counters[5], checked);
+}
+
 }  // namespace
 }  // namespace cck
 
@@ -137,5 +207,11 @@ extern "C" int32_t cck_div_selftest(const float* xs, int64_t nx, const float* ss
   if (nx <= 0 || ns <= 0) return (int32_t)hipSuccess;
   hipStream_t st = static_cast<hipStream_t>(stream);
   div_selftest<<<flat_grid(nx * ns / 16, 256, 8192), 256, 0, st>>>(xs, nx, ss, ns, counters);
+  return launch_status();
+}
+
+extern "C" int32_t cck_silu_table_selftest(unsigned long long* counters, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  silu_table_selftest<<<1, 1024, 0, st>>>(counters);
   return launch_status();
 }

@@ -9,236 +9,27 @@
 // (dynamic, per token) or with a static scale and does not write y itself.
 //
 // Design: the plain op is a flat grid-stride stream of 16-byte vectors (two
-// loads, one store per vector). The FP8 variant is row-resident: one
+// loads, one store per vector) with the arithmetic SiLU of silu.hpp. The FP8
+// variants add the FP8 conversion per element, which makes them VALU-bound
+// with the arithmetic SiLU; for bf16 they look the SiLU up in the LDS table
+// instead (silu.hpp). The per-token FP8 variant is row-resident: one
 // workgroup per row keeps y in registers while it reduces the row amax, so
 // gate/up are read once and only the codes and the scale are written.
-//
-// The op is close to VALU-bound on gfx950 (no packed fp32 here), so sigmoid is
-// built for instruction count: exp(-g) = 2^th * (1 + c) with one v_exp_f32,
-// and 1/(1+e) = one v_rcp_f32 plus a Newton step. For bf16 inputs, th = -g*HI
-// is exact (8-bit g times a 16-bit HI), so only the tiny c = -g*LO*ln2 is
-// rounded; other input types split the product with an fma. Vectors with a
-// gate outside the fast range (exp(-g) near overflow, sigmoid subnormal, the
-// first-order correction no longer within an ulp, inf / NaN) use the IEEE
-// expf / division path.
 #include "launch.hpp"
+#include "silu.hpp"
 
 namespace cck {
 namespace {
 
-#pragma clang fp contract(off)
-
-// log2(e) = HI + LO; HI has 16 significant bits so g * HI is exact for bf16 g.
-template <class C>
-struct SiluConsts {
-  static constexpr bool kExactHi = false;
-  static constexpr float kHi = 1.44269502162933349609375f;  // RN32(log2 e)
-  static constexpr float kLo = 1.925963033500011e-08f;       // log2 e - kHi
-  static constexpr float kFastAbs = 87.0f;                   // sigmoid stays normal
-};
-template <>
-struct SiluConsts<CodecBF16> {
-  static constexpr bool kExactHi = true;
-  static constexpr float kHi = 1.44268798828125f;
-  static constexpr float kLoLn2 = 4.888495368504664e-06f;  // (log2 e - kHi) * ln 2
-  // First-order correction 1 + c is within an ulp for |c| < 1e-4 (|g| < 20).
-  static constexpr float kFastAbs = 20.0f;
-};
-
-constexpr float kLn2 = 0.693147182464599609375f;
-
-template <class C>
-__device__ inline float exp_neg_fast(float g) {
-  using K = SiluConsts<C>;
-  if constexpr (K::kExactHi) {
-    const float th = g * -K::kHi;  // exact
-    const float c = g * -K::kLoLn2;
-    const float p = __builtin_amdgcn_exp2f(th);
-    return __builtin_fmaf(p, c, p);
-  } else {
-    const float th = g * -K::kHi;
-    const float rem = __builtin_fmaf(g, -K::kHi, -th);  // exact remainder of the product
-    const float tl = __builtin_fmaf(g, -K::kLo, rem);
-    const float p = __builtin_amdgcn_exp2f(th);
-    return __builtin_fmaf(p, tl * kLn2, p);
-  }
-}
-
-// 1 / d to within an ulp: v_rcp_f32 then one Newton step with a fused remainder.
-__device__ inline float recip_refined(float d) {
-  const float r0 = __builtin_amdgcn_rcpf(d);
-  const float e = __builtin_fmaf(-d, r0, 1.0f);
-  return __builtin_fmaf(e, r0, r0);
-}
-
-__device__ inline float silu_exact(float g) { return g * (1.0f / (1.0f + __builtin_expf(-g))); }
-
-template <class C>
-__device__ inline float silu_fast(float g) {
-  return g * recip_refined(1.0f + exp_neg_fast<C>(g));
-}
-
-// SiLU of one element: the fast form inside its range, the exact form
-// elsewhere. Every path below computes exactly this per element, whatever
-// the neighbouring elements are.
-template <class C>
-__device__ inline float silu_one(float g) {
-  return __builtin_fabsf(g) <= SiluConsts<C>::kFastAbs ? silu_fast<C>(g) : silu_exact(g);
-}
-
-// In place: g[i] <- T(silu(g[i])) * u[i], i.e. y before its final rounding.
-// A vector whose |g| are all <= kFastAbs (one v_maximum3_f32 per two
-// elements, NaN-propagating) takes the fast form without per-element selects.
-template <class C>
-__device__ inline void swiglu_math(float (&g)[C::VEC], const float (&u)[C::VEC]) {
-  constexpr int VEC = C::VEC;
-  float mx = 0.0f;
-#pragma unroll
-  for (int i = 0; i < VEC; i += 2) mx = absmax2(mx, g[i], g[i + 1]);
-  if (mx <= SiluConsts<C>::kFastAbs) {
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) g[i] = silu_fast<C>(g[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) g[i] = silu_one<C>(g[i]);
-  }
-#pragma unroll
-  for (int i = 0; i < VEC; i += 2) C::round2(g[i], g[i + 1]);
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) g[i] = g[i] * u[i];
-}
-
-// ---------------------------------------------------------------------------
-// bf16 SiLU table in LDS.
-//
-// A bf16 gate has only 2^16 values, so T(silu(g)) is a function of its 16
-// bits. The common range 2^-14 <= |g| < 32 (4864 values) is tabulated per
-// workgroup in LDS (19 KB of fp32, filled with silu_one at workgroup start),
-// which replaces the two transcendental instructions and the Newton step per
-// element by one ds_read_b32. Vectors with a gate outside the range (zeros,
-// tiny or huge values, inf/NaN) fall back to silu_one, so results are
-// bit-identical to the arithmetic path.
-//
-// Key of a bf16 pattern b with magnitude field m = b & 0x7fff and sign s:
-// 2 * (m - kLo) + s, i.e. the 16-bit pattern rotated left by one minus
-// 2 * kLo; two keys are formed per packed word with one v_pk_sub_u16.
-// ---------------------------------------------------------------------------
-struct SiluTableBF16 {
-  static constexpr uint32_t kLo = 0x3880;                    // 2^-14
-  static constexpr uint32_t kHi = 0x4200;                    // 32.0
-  static constexpr uint32_t kEntries = 2 * (kHi - kLo);      // 4864
-
-  // Rounded SiLU of every tabulated value. Two fills of identical contents
-  // (the table kernels equal the arithmetic kernels for all 2^16 gates, so
-  // both equal silu_one); which one a kernel uses was measured on MI355X.
-  // * |g| < 2^-9: sigmoid(g) = 1/2 + g/4 + O(g^3), so g*sigmoid(g) = (g/2)(1 + d)
-  //   with |d| < 2^-10, inside half a bf16 ulp of the exactly representable g/2:
-  //   those entries are g/2 without evaluating the SiLU (a wave-uniform branch).
-  // * g > kFastAbs: silu(g) = g exactly (exp(-g) < 2^-25, so 1 + exp(-g) rounds
-  //   to 1 in silu_exact).
-  //
-  // fill_single: one entry per thread and step, silu_one otherwise.
-  static constexpr uint32_t kTinyKeys = 2 * (0x3b00 - kLo);  // |g| < 2^-9
-  __device__ static void fill_single(float* tab, int tid, int nthreads) {
-    for (uint32_t i = tid; i < kEntries; i += nthreads) {
-      const uint32_t key = i + 2 * kLo;
-      const float g = bits_f32((((key & 1u) << 15) | (key >> 1)) << 16);
-      float v;
-      if (i < kTinyKeys) {
-        v = g * 0.5f;
-      } else if (g > SiluConsts<CodecBF16>::kFastAbs) {
-        v = g;
-      } else {
-        v = CodecBF16::round(silu_one<CodecBF16>(g));
-      }
-      tab[i] = v;
-    }
-  }
-
-  // fill_pairs: the (+a, -a) pair of adjacent keys 2p, 2p + 1 (magnitude field
-  // kLo + p) per thread and step. For a <= kFastAbs, e = exp(-a) and
-  // r = 1/(1+e) serve both signs, since sigmoid(-a) = e * r:
-  // silu(+a) = a*r, silu(-a) = -a*(e*r); rounded to bf16 this equals silu_one
-  // on both signs for every bf16 magnitude in range (checked exhaustively on
-  // the device), at one exp and one reciprocal per pair instead of per entry.
-  static constexpr uint32_t kPairs = kHi - kLo;
-  static constexpr uint32_t kTinyPairs = 0x3b00 - kLo;  // a < 2^-9
-  __device__ static void fill_pairs(float* tab, int tid, int nthreads) {
-    using K = SiluConsts<CodecBF16>;
-    for (uint32_t p = tid; p < kPairs; p += nthreads) {
-      const float a = bits_f32((kLo + p) << 16);
-      float pos, neg;
-      if (p < kTinyPairs) {
-        pos = a * 0.5f;
-        neg = -a * 0.5f;
-      } else if (a <= K::kFastAbs) {
-        const float e = exp_neg_fast<CodecBF16>(a);
-        const float r = recip_refined(1.0f + e);
-        pos = CodecBF16::round(a * r);
-        neg = CodecBF16::round(-a * (e * r));
-      } else {
-        pos = a;
-        neg = CodecBF16::round(silu_one<CodecBF16>(-a));
-      }
-      *reinterpret_cast<f32x2*>(tab + 2 * p) = (f32x2){pos, neg};
-    }
-  }
-
-  __device__ static uint32_t keys2(uint32_t w) {
-    const uint32_t rot = ((w << 1) & 0xfffefffeu) | ((w >> 15) & 0x00010001u);
-    const u16x2 k = __builtin_bit_cast(u16x2, rot) - (u16x2){(uint16_t)(2 * kLo), (uint16_t)(2 * kLo)};
-    return __builtin_bit_cast(uint32_t, k);
-  }
-
-  // a[i] <- T(silu(g[i])) for the 8 gates of w; false (a untouched) when any
-  // gate is outside the table.
-  __device__ static bool lookup8(const u32x4& w, const float* tab, float (&a)[8]) {
-    uint32_t key[4];
-    uint32_t mx = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      key[j] = keys2(w[j]);
-      mx = pk_max_u16(mx, key[j]);
-    }
-    if (max(mx & 0xffffu, mx >> 16) >= kEntries) return false;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      a[2 * j] = tab[key[j] & 0xffffu];
-      a[2 * j + 1] = tab[key[j] >> 16];
-    }
-    return true;
-  }
-};
-
-// T(silu(g[i])) for one 16-byte vector of gates, from the table when given.
-template <class C, bool TAB>
-__device__ inline void silu_vec(const u32x4& gw, const float* tab, float (&a)[C::VEC]) {
-  if constexpr (TAB) {
-    if (SiluTableBF16::lookup8(gw, tab, a)) return;
-  }
-  C::unpack(gw, a);
-  float mx = 0.0f;
-#pragma unroll
-  for (int i = 0; i < C::VEC; i += 2) mx = absmax2(mx, a[i], a[i + 1]);
-  if (mx <= SiluConsts<C>::kFastAbs) {
-#pragma unroll
-    for (int i = 0; i < C::VEC; ++i) a[i] = silu_fast<C>(a[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < C::VEC; ++i) a[i] = silu_one<C>(a[i]);
-  }
-#pragma unroll
-  for (int i = 0; i < C::VEC; i += 2) C::round2(a[i], a[i + 1]);
-}
-
 // The plain op: a grid-stride stream of 16-byte vectors, UNROLL per thread
-// per step. With TAB (bf16), each workgroup first fills the SiLU table; the
-// loads of its first step are issued before the fill so they overlap it.
-template <class C, int THREADS, int UNROLL, bool TAB>
+// per step, the next step's loads issued before this step's math. It uses the
+// arithmetic SiLU for every dtype: with the LDS table (and its per-workgroup
+// fill) the bf16 stream measured slower on MI355X (111.4 vs 109.9 us at
+// 8192 x 14336, 233.8 vs 218.8 us at 16384 x 14336).
+template <class C, int THREADS, int UNROLL>
 __global__ __launch_bounds__(THREADS) void swiglu_flat(const u32x4* __restrict__ gate,
                                                        const u32x4* __restrict__ up,
                                                        u32x4* __restrict__ y, int64_t nvec) {
-  __shared__ __attribute__((aligned(16))) float tab[TAB ? SiluTableBF16::kEntries : 1];
   const int64_t stride = (int64_t)gridDim.x * THREADS * UNROLL;
   int64_t base = (int64_t)blockIdx.x * THREADS * UNROLL + threadIdx.x;
   u32x4 g[UNROLL], u[UNROLL];
@@ -253,17 +44,13 @@ __global__ __launch_bounds__(THREADS) void swiglu_flat(const u32x4* __restrict__
     }
   };
   load(base);
-  if constexpr (TAB) {
-    SiluTableBF16::fill_single(tab, threadIdx.x, THREADS);
-    __syncthreads();
-  }
   for (; base < nvec; base += stride) {
 #pragma unroll
     for (int k = 0; k < UNROLL; ++k) {
       const int64_t v = base + k * THREADS;
       if (v < nvec) {
         float a[C::VEC], uf[C::VEC];
-        silu_vec<C, TAB>(g[k], tab, a);
+        silu_vec<C, false>(g[k], nullptr, a);
         C::unpack(u[k], uf);
 #pragma unroll
         for (int i = 0; i < C::VEC; ++i) a[i] = a[i] * uf[i];
@@ -507,9 +294,9 @@ int32_t launch_swiglu_fp8_token(const void* gate, const void* up, uint8_t* yq, f
   return launch_status();
 }
 
-// Streams of at least this many 16-byte vectors (1M bf16 elements) use the
-// SiLU table: 1024-thread workgroups of two vectors per thread, so one table
-// fill serves 16384 elements.
+// Static-scale FP8 streams of at least this many 16-byte vectors (1M bf16
+// elements) use the SiLU table: 1024-thread workgroups of two vectors per
+// thread, so one table fill serves 16384 elements.
 constexpr int64_t kTabMinVec = int64_t(1) << 17;
 constexpr int kTabThreads = 1024, kTabUnroll = 2;
 
@@ -531,18 +318,9 @@ extern "C" int32_t launch_swiglu_fwd(const void* gate, const void* up, void* y, 
       const u32x4* g4 = static_cast<const u32x4*>(gate);
       const u32x4* u4 = static_cast<const u32x4*>(up);
       u32x4* y4 = static_cast<u32x4*>(y);
-      bool tab = false;
-      if constexpr (std::is_same_v<C, CodecBF16>) {
-        if (nvec >= kTabMinVec) {
-          constexpr int kPer = kTabThreads * kTabUnroll;
-          swiglu_flat<C, kTabThreads, kTabUnroll, true>
-              <<<flat_grid((nvec + kPer - 1) / kPer, 1, 1 << 20), kTabThreads, 0, st>>>(g4, u4, y4, nvec);
-          tab = true;
-        }
-      }
-      if (!tab && nvec > 0) {
+      if (nvec > 0) {
         constexpr int UNROLL = 4;
-        swiglu_flat<C, 256, UNROLL, false>
+        swiglu_flat<C, 256, UNROLL>
             <<<flat_grid((nvec + UNROLL - 1) / UNROLL, 256, 1 << 20), 256, 0, st>>>(g4, u4, y4, nvec);
       }
       done = nvec * C::VEC;

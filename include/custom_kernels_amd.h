@@ -170,6 +170,13 @@ int32_t cck_div_selftest(const float* xs, int64_t nx, const float* ss, int64_t n
 int32_t cck_scale_selftest(uint64_t start, uint64_t count, int32_t fp8_format,
                            unsigned long long* counters, void* stream);
 
+/* Checks the bf16 SiLU table of the SwiGLU+FP8 kernels: both fills against the
+ * arithmetic SiLU for every entry, and the table lookup against the arithmetic
+ * path for all 2^16 bf16 gates. counters: 6 x u64, zeroed, with [2] preset to
+ * UINT64_MAX; [0], [1], [3] are mismatch counts; see csrc/selftest.hip for the
+ * layout. */
+int32_t cck_silu_table_selftest(unsigned long long* counters, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

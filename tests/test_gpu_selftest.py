@@ -9,7 +9,11 @@ run through the C ABI diagnostics (csrc/selftest.hip):
   dynamic scale a bf16 amax can produce, and edge scales);
 * the dynamic scale clamp(amax / FP8_MAX, 1e-12) computed with the exact
   power-of-two step and the fma-corrected division by 7, against IEEE
-  division, for every non-negative fp32 amax (2^31 patterns incl. inf / NaN).
+  division, for every non-negative fp32 amax (2^31 patterns incl. inf / NaN);
+* the bf16 SiLU table of the SwiGLU+FP8 kernels: both fills against the
+  arithmetic SiLU entry by entry, and the table lookup against the arithmetic
+  path for all 2^16 bf16 gates (the arithmetic path itself is checked against
+  the oracle for every bf16 gate in test_swiglu_gpu.py).
 """
 
 from __future__ import annotations
@@ -104,3 +108,19 @@ def test_dynamic_scale_matches_ieee_division_for_every_amax(fmt):
     torch.cuda.synchronize()
     c = counters.cpu().numpy().view(np.uint64)
     assert c[0] == 0, f"{c[0]} scale mismatches, lowest amax bits {hex(int(c[1]))}"
+
+
+def test_silu_table_equals_arithmetic_silu():
+    lib = _cck.load()
+    counters = torch.zeros(6, dtype=torch.int64, device="cuda")
+    counters[2] = -1
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.cck_silu_table_selftest(counters.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    c = counters.cpu().numpy().view(np.uint64)
+    assert c[5] == 2 * 65536
+    # Both groupings exercise the table and the fallback: the ascending one
+    # has whole vectors in range, the permuted one mixes ranges.
+    assert 0 < c[4] < 2 * 65536 // 8
+    assert c[0] == 0 and c[1] == 0, f"fill mismatches {c[0]}/{c[1]}, lowest index {int(c[2])}"
+    assert c[3] == 0, f"{c[3]} lookups differ from the arithmetic SiLU"
