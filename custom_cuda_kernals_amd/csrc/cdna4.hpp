@@ -416,49 +416,14 @@ __device__ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) ==
 #ifndef CCK_STREAM_NT_STORE
 #define CCK_STREAM_NT_STORE 1
 #endif
-// One row of a tensor, addressed by 32-bit byte offsets. RowBuf<true> is a
-// raw buffer resource (base and size in SGPRs, no per-lane 64-bit address
-// arithmetic, accesses past `bytes` read 0 / are dropped by the hardware range
-// check); RowBuf<false> is a plain global pointer. Which one a row kernel uses
-// was measured per kernel on MI355X. Rows are at most a few hundred KB here.
-constexpr int kBufDword3 = 0x00020000;  // gfx9 family: DATA_FORMAT_32, no swizzle
-constexpr int kBufLoadPolicy = CCK_STREAM_NT_LOAD ? 2 : 0;   // nt
-constexpr int kBufStorePolicy = CCK_STREAM_NT_STORE ? 2 : 0;  // nt
 
-template <bool RSRC>
-struct RowBuf;
-
-// Raw buffer resource: base and size in SGPRs, 32-bit lane offsets, hardware
-// range check.
-template <>
-struct RowBuf<true> {
-  __amdgpu_buffer_rsrc_t r;
-  __device__ RowBuf(const void* base, uint32_t bytes)
-      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufDword3)) {}
-  __device__ u32x4 ld16(uint32_t off) const {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufLoadPolicy));
-  }
-  __device__ void st16(const u32x4& v, uint32_t off) const {
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kBufStorePolicy);
-  }
-  __device__ void st8(const u32x2& v, uint32_t off) const {
-    __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, kBufStorePolicy);
-  }
-  __device__ void st4(uint32_t v, uint32_t off) const {
-    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kBufStorePolicy);
-  }
-};
-
-// The same interface over global pointers (callers guard the row end).
-template <>
-struct RowBuf<false> {
-  char* p;
-  __device__ RowBuf(const void* base, uint32_t) : p(static_cast<char*>(const_cast<void*>(base))) {}
-  __device__ u32x4 ld16(uint32_t off) const;
-  __device__ void st16(const u32x4& v, uint32_t off) const;
-  __device__ void st8(const u32x2& v, uint32_t off) const;
-  __device__ void st4(uint32_t v, uint32_t off) const;
-};
+// Cache-policy immediate of gfx950 vector memory instructions (the aux
+// operand of the buffer builtins): SC0 = 1, NT = 2, SC1 = 16. On stores,
+// SC1 / SC0 select the scope the write is made visible at (write-through
+// beyond the CU's caches) and NT marks it as streaming.
+constexpr int kPolSC0 = 1, kPolNT = 2, kPolSC1 = 16;
+constexpr int kBufLoadPolicy = CCK_STREAM_NT_LOAD ? kPolNT : 0;
+constexpr int kBufStorePolicy = CCK_STREAM_NT_STORE ? kPolNT : 0;
 
 template <class T>
 __device__ inline T ld_stream(const T* p) {
@@ -477,17 +442,46 @@ __device__ inline void st_stream(T v, T* p) {
   }
 }
 
-__device__ inline u32x4 RowBuf<false>::ld16(uint32_t off) const {
-  return ld_stream(reinterpret_cast<const u32x4*>(p + off));
-}
-__device__ inline void RowBuf<false>::st16(const u32x4& v, uint32_t off) const {
-  st_stream(v, reinterpret_cast<u32x4*>(p + off));
-}
-__device__ inline void RowBuf<false>::st8(const u32x2& v, uint32_t off) const {
-  st_stream(v, reinterpret_cast<u32x2*>(p + off));
-}
-__device__ inline void RowBuf<false>::st4(uint32_t v, uint32_t off) const {
-  st_stream(v, reinterpret_cast<uint32_t*>(p + off));
-}
+// One row of a tensor, addressed by 32-bit byte offsets. RowBuf<true> is a
+// raw buffer resource (base and size in SGPRs, no per-lane 64-bit address
+// arithmetic, accesses past `bytes` read 0 / are dropped by the hardware range
+// check); RowBuf<false> is a plain global pointer. Which one a row kernel uses
+// was measured per kernel on MI355X. Rows are at most a few hundred KB here.
+// SPOL is the cache policy of the row's stores (buffer resources only).
+constexpr int kBufDword3 = 0x00020000;  // gfx9 family: DATA_FORMAT_32, no swizzle
+
+template <bool RSRC, int SPOL = kBufStorePolicy>
+struct RowBuf;
+
+template <int SPOL>
+struct RowBuf<true, SPOL> {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ RowBuf(const void* base, uint32_t bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufDword3)) {}
+  __device__ u32x4 ld16(uint32_t off) const {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufLoadPolicy));
+  }
+  __device__ void st16(const u32x4& v, uint32_t off) const {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, SPOL);
+  }
+  __device__ void st8(const u32x2& v, uint32_t off) const {
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, SPOL);
+  }
+  __device__ void st4(uint32_t v, uint32_t off) const {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, SPOL);
+  }
+};
+
+// The same interface over global pointers (callers guard the row end).
+template <int SPOL>
+struct RowBuf<false, SPOL> {
+  static_assert(SPOL == kBufStorePolicy, "global-pointer rows store with the streaming policy");
+  char* p;
+  __device__ RowBuf(const void* base, uint32_t) : p(static_cast<char*>(const_cast<void*>(base))) {}
+  __device__ u32x4 ld16(uint32_t off) const { return ld_stream(reinterpret_cast<const u32x4*>(p + off)); }
+  __device__ void st16(const u32x4& v, uint32_t off) const { st_stream(v, reinterpret_cast<u32x4*>(p + off)); }
+  __device__ void st8(const u32x2& v, uint32_t off) const { st_stream(v, reinterpret_cast<u32x2*>(p + off)); }
+  __device__ void st4(uint32_t v, uint32_t off) const { st_stream(v, reinterpret_cast<uint32_t*>(p + off)); }
+};
 
 }  // namespace cck

@@ -62,6 +62,9 @@ struct AmaxOp<CodecF32> {
   using type = MaxU32;
 };
 
+// Cache policy of the per-token kernel's code stores.
+constexpr int kPolTokenQ = kBufStorePolicy;
+
 // ---------------------------------------------------------------------------
 // Token granularity, register-resident rows: one workgroup per row, each
 // thread holds ITEMS 16-byte vectors. Requires cols % VEC == 0 and 16-byte
@@ -98,7 +101,7 @@ __global__ __launch_bounds__(THREADS) void fp8_token_resident(const void* __rest
     const float r = 1.0f / s;
     if (threadIdx.x == 0) scale[row] = s;
     const bool fast = fast_path_ok<FMT>(s, r, amax);
-    const RowBuf<true> bq(q + row * cols, (uint32_t)cols);
+    const RowBuf<true, kPolTokenQ> bq(q + row * cols, (uint32_t)cols);
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       const uint32_t v = threadIdx.x + k * THREADS;

@@ -22,6 +22,16 @@ namespace {
 
 #pragma clang fp contract(off)
 
+// Cache policies of the row stores, per MODE (below), measured on MI355X
+// against NT on both streams at the config shapes:
+//   MODE 0, [8192, 4096] bf16: residual_out SC1|NT and y SC1, 43.7 vs 44.1-44.7 us;
+//   MODE 1, [16384, 4096]: NT on both (every SC1 combination 0.3-1 % slower);
+//   MODE 2, [16384, 4096]: SC1|NT on both, 74.4 vs 75.4 us.
+constexpr int ro_store_policy(int mode) { return mode == 1 ? kPolNT : (kPolSC1 | kPolNT); }
+constexpr int out_store_policy(int mode) {
+  return mode == 0 ? kPolSC1 : mode == 1 ? kPolNT : (kPolSC1 | kPolNT);
+}
+
 // f[i] <- T(f[i] * inv) * w[i]  (the product is rounded by the caller's store).
 template <class C>
 __device__ inline void scale_round_mul(float (&f)[C::VEC], float inv, const float (&w)[C::VEC]) {
@@ -83,7 +93,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
   // contiguous block of rows (65 % vs 75 % of peak at [8192, 4096] bf16).
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x, parity ^= 1) {
     const int64_t off = row * cols * C::kBytes;
-    const RowBuf<true> bro(static_cast<char*>(ro) + off, row_bytes);
+    const RowBuf<true, ro_store_policy(MODE)> bro(static_cast<char*>(ro) + off, row_bytes);
     u32x4 xa[ITEMS], ra[ITEMS];
     load_row(row, xa, ra);
     u32x4 rov[ITEMS];
@@ -120,7 +130,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
     const float inv = 1.0f / __builtin_sqrtf(variance + eps);
 
     if constexpr (MODE == 0) {
-      const RowBuf<true> by(static_cast<char*>(y) + off, row_bytes);
+      const RowBuf<true, out_store_policy(MODE)> by(static_cast<char*>(y) + off, row_bytes);
 #pragma unroll
       for (int k = 0; k < ITEMS; ++k) {
         const int v = threadIdx.x + k * THREADS;
@@ -163,7 +173,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
       }
       const float r = 1.0f / s;
       const bool fast = fast_path_ok<FMT>(s, r, amax);
-      const RowBuf<true> bq(yq + row * cols, (uint32_t)cols);
+      const RowBuf<true, out_store_policy(MODE)> bq(yq + row * cols, (uint32_t)cols);
 #pragma unroll
       for (int k = 0; k < ITEMS; ++k) {
         const int v = threadIdx.x + k * THREADS;

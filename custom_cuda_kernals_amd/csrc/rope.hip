@@ -20,6 +20,13 @@ namespace {
 
 #pragma clang fp contract(off)
 
+// Stores of a one-token-per-workgroup launch (TOK == 1) go through per-token
+// buffer resources with SC1|NT: 104.0 vs 104.7 us with global-pointer NT
+// stores at config 4 on MI355X. With several tokens per workgroup the row
+// base is not wave-uniform, so those use global pointers.
+template <int TOK>
+using RopeRow = RowBuf<TOK == 1, TOK == 1 ? (kPolSC1 | kPolNT) : kBufStorePolicy>;
+
 template <class C, int CHUNKS, int TOK>
 __global__ __launch_bounds__(256) void rope_tokens(const void* __restrict__ q, const void* __restrict__ k,
                                                    const float* __restrict__ cos_t,
@@ -29,11 +36,14 @@ __global__ __launch_bounds__(256) void rope_tokens(const void* __restrict__ q, c
   constexpr int VEC = C::VEC;
   constexpr int LANES = 256 / TOK;          // threads per token
   constexpr int HLANES = LANES / CHUNKS;    // head lanes per token
-  const int t_local = threadIdx.x / LANES;
+  const int t_local = TOK == 1 ? 0 : threadIdx.x / LANES;
   const int c = threadIdx.x % CHUNKS;
   const int hl = (threadIdx.x % LANES) / CHUNKS;
   const int half = head_dim / 2;
   const int heads = hq + hkv;
+  // Token rows are below 2 GiB (checked by the launcher), so 32-bit offsets hold.
+  const uint32_t q_bytes = (uint32_t)((int64_t)hq * head_dim * C::kBytes);
+  const uint32_t k_bytes = (uint32_t)((int64_t)hkv * head_dim * C::kBytes);
   for (int64_t tok = (int64_t)blockIdx.x * TOK + t_local; tok < tokens; tok += (int64_t)gridDim.x * TOK) {
     const int64_t s = tok % seq_len;
     float cs[VEC], sn[VEC];
@@ -45,25 +55,28 @@ __global__ __launch_bounds__(256) void rope_tokens(const void* __restrict__ q, c
       cs[4 * i] = a.x; cs[4 * i + 1] = a.y; cs[4 * i + 2] = a.z; cs[4 * i + 3] = a.w;
       sn[4 * i] = b.x; sn[4 * i + 1] = b.y; sn[4 * i + 2] = b.z; sn[4 * i + 3] = b.w;
     }
-    for (int h = hl; h < heads; h += HLANES) {
-      const bool is_q = h < hq;
-      const char* src = is_q ? static_cast<const char*>(q) : static_cast<const char*>(k);
-      char* dst = is_q ? static_cast<char*>(q_out) : static_cast<char*>(k_out);
-      const int64_t row = is_q ? tok * hq + h : tok * hkv + (h - hq);
-      const int64_t e0 = row * head_dim + c * VEC;
-      const u32x4* p1 = reinterpret_cast<const u32x4*>(src + e0 * C::kBytes);
-      const u32x4* p2 = reinterpret_cast<const u32x4*>(src + (e0 + half) * C::kBytes);
+    // Head hh of one tensor's token row: both halves are read before either
+    // is written, so the rotation works in place.
+    auto rotate = [&](const char* src, const RopeRow<TOK>& dst, int hh) {
+      const uint32_t off = (uint32_t)((hh * head_dim + c * VEC) * C::kBytes);
       float x1[VEC], x2[VEC], o1[VEC], o2[VEC];
-      C::unpack(ld_stream(p1), x1);
-      C::unpack(ld_stream(p2), x2);
+      C::unpack(ld_stream(reinterpret_cast<const u32x4*>(src + off)), x1);
+      C::unpack(ld_stream(reinterpret_cast<const u32x4*>(src + off + half * C::kBytes)), x2);
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
         o1[i] = x1[i] * cs[i] - x2[i] * sn[i];
         o2[i] = x2[i] * cs[i] + x1[i] * sn[i];
       }
-      st_stream(C::pack(o1), reinterpret_cast<u32x4*>(dst + e0 * C::kBytes));
-      st_stream(C::pack(o2), reinterpret_cast<u32x4*>(dst + (e0 + half) * C::kBytes));
-    }
+      dst.st16(C::pack(o1), off);
+      dst.st16(C::pack(o2), off + half * C::kBytes);
+    };
+    const RopeRow<TOK> qo(static_cast<char*>(q_out) + tok * q_bytes, q_bytes);
+    const RopeRow<TOK> ko(static_cast<char*>(k_out) + tok * k_bytes, k_bytes);
+    // Heads h = hl, hl + HLANES, ...: the q heads, then the k heads (separate
+    // loops keep each loop's row resource uniform).
+    int h = hl;
+    for (; h < hq; h += HLANES) rotate(static_cast<const char*>(q) + tok * q_bytes, qo, h);
+    for (; h < heads; h += HLANES) rotate(static_cast<const char*>(k) + tok * k_bytes, ko, h - hq);
   }
 }
 
@@ -119,7 +132,8 @@ extern "C" int32_t launch_rope_fwd(const void* q, const void* k, const void* cos
     const bool vec_ok = (half % C::VEC == 0) && host_aligned(q, 16) && host_aligned(k, 16) &&
                         host_aligned(q_out, 16) && host_aligned(k_out, 16) &&
                         host_aligned(ct, 16) && host_aligned(sn, 16);
-    const int chunks = vec_ok ? half / C::VEC : 0;
+    const int64_t max_row_bytes = (int64_t)(hq > hkv ? hq : hkv) * d * C::kBytes;
+    const int chunks = vec_ok && max_row_bytes <= 0x7fffffff ? half / C::VEC : 0;
     // TOK tokens per workgroup, 256/TOK threads per token, CHUNKS chunk lanes.
 #define CCK_ROPE(CH_, TOK_)                                                                  \
   rope_tokens<C, CH_, TOK_><<<flat_grid(tokens, TOK_, 1 << 30), 256, 0, st>>>(             \

@@ -154,6 +154,12 @@ __global__ __launch_bounds__(256) void swiglu_fp8_static_scalar(const void* __re
   }
 }
 
+// Code stores of the per-token variant: a buffer resource with SC1|NT, measured
+// on MI355X against global-pointer NT stores: 90.4 vs 90.8 us at
+// [8192, 14336], 177.8 vs 179.2 us at [16384, 14336].
+constexpr bool kRsrcQ = true;
+constexpr int kPolQ = kPolSC1 | kPolNT;
+
 // Per-token FP8 variant, register-resident rows; y is kept as floats (already
 // rounded to T) between the amax reduction and the quantisation. TAB (bf16)
 // selects the LDS SiLU table, filled while the first row's loads are in
@@ -219,7 +225,7 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
     if (threadIdx.x == 0) scale[row] = s;
     const float r = 1.0f / s;
     const bool fast = fast_path_ok<FMT>(s, r, amax);
-    const RowBuf<false> bq(yq + row * cols, (uint32_t)cols);
+    const RowBuf<kRsrcQ, kPolQ> bq(yq + row * cols, (uint32_t)cols);
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       const uint32_t v = threadIdx.x + k * THREADS;
