@@ -98,6 +98,27 @@ def _ops(torch, native):
     ops.append(Op("fp8_quant_token", "fp8_token_bf16_2048x4096", m1 * n1 * 3 + m1 * 4, mk1,
                   lambda b: native.fp8_quant_token_fwd(b["x"], b["q"], b["s"], "e4m3"), m1 * n1 * 3, [m1, n1]))
 
+    # The reference's own two granularities on the config-1 input (drop-ins, not BASELINE
+    # configs): 128x128 tiles, and one dynamic scale for the tensor, whose caller-zeroed
+    # int32 amax scratch is cleared inside the timed op as the reference's wrapper does
+    # (custom_cuda/kernels/fp8_quant.py:51-62).
+    tiles = (math.ceil(m1 / 128), math.ceil(n1 / 128))
+
+    def mk1g():
+        d = mk1()
+        d.update(sb=torch.empty(tiles, device=dev), st=torch.empty(1, device=dev),
+                 amax=torch.zeros(1, dtype=torch.int32, device=dev))
+        return d
+
+    def tensor_fp8(b):
+        b["amax"].zero_()
+        native.fp8_quant_tensor_fwd(b["x"], b["q"], b["st"], b["amax"], "e4m3")
+
+    ops.append(Op("fp8_quant_block", "fp8_block128_bf16_2048x4096", m1 * n1 * 3 + tiles[0] * tiles[1] * 4, mk1g,
+                  lambda b: native.fp8_quant_block_fwd(b["x"], b["q"], b["sb"], "e4m3"), m1 * n1 * 3, [m1, n1]))
+    ops.append(Op("fp8_quant_tensor", "fp8_tensor_bf16_2048x4096", m1 * n1 * 3 + 8, mk1g, tensor_fp8, m1 * n1 * 3,
+                  [m1, n1]))
+
     # 2: RMSNorm + residual, [8192, 4096] bf16, eps 1e-5
     m2, n2 = 8192, 4096
     w2 = (1.0 + 0.1 * torch.randn(n2, device=dev, generator=g)).to(bf16)

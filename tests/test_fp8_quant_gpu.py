@@ -139,3 +139,89 @@ def test_rejects_bad_format_and_granularity():
         fp8_quant(x, "e4m3", "row")
     with pytest.raises(ValueError):
         fp8_quant(x, "e4m3", "block", scale=0.1)
+
+
+# ---- Tensor granularity: the three-step maximum (per-workgroup partial maxima
+# in the codes buffer, one finishing atomicMax into the caller's int32, then
+# the cast), exercised through the C ABI where the Python API cannot reach.
+
+@pytest.mark.parametrize("where", ["first", "middle", "last"])
+@pytest.mark.parametrize("shape", [(1, 1), (1, 3), (2, 3), (3, 1001), (4099, 4097)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_tensor_amax_found_anywhere(shape, where):
+    """The largest |x| at the first, middle or last element: sizes below the
+    partial-slot minimum, a scalar tail after the 16-byte vectors, and a grid
+    of 512 partial workgroups that each stride over several vectors."""
+    x = inputs.randn(shape, torch.bfloat16, seed=shape[0] * 31 + shape[1])
+    flat = x.view(-1)
+    idx = {"first": 0, "middle": flat.numel() // 2, "last": flat.numel() - 1}[where]
+    flat[idx] = -1000.0
+    _check(x, "e4m3", "tensor")
+
+
+def _tensor_abi(x_dev: torch.Tensor, q: torch.Tensor, scratch: torch.Tensor, fmt_tag: int = 3):
+    from tests import _cck
+
+    lib = _cck.load()
+    scale = torch.empty(1, dtype=torch.float32, device="cuda")
+    m, n = x_dev.shape
+    dtag = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[x_dev.dtype]
+    rc = lib.launch_fp8_quant_tensor_fwd(x_dev.data_ptr(), q.data_ptr(), scale.data_ptr(), scratch.data_ptr(), m, n,
+                                         dtag, fmt_tag, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    return scale
+
+
+@pytest.mark.parametrize("offset", [1, 2, 3])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+def test_tensor_codes_buffer_unaligned(offset, dtype):
+    """A codes buffer that is not 4-byte aligned: the partial slots are placed
+    at the first aligned word inside it, and every code is still written."""
+    m, n = 700, 1003
+    x = inputs.randn((m, n), dtype, seed=offset)
+    buf = torch.full((m * n + 8,), 0x55, dtype=torch.uint8, device="cuda")
+    q = buf[offset:offset + m * n]
+    assert q.data_ptr() % 4 != 0
+    scratch = torch.zeros(1, dtype=torch.int32, device="cuda")
+    scale = _tensor_abi(x.cuda(), q, scratch)
+    codes, s_ref = ofp8.quant_tensor(x.float().numpy(), "e4m3")
+    assert_codes_equal(q, codes.reshape(-1))
+    assert_f32_bits_equal(scale, s_ref)
+    b = buf.cpu().numpy()
+    assert (b[:offset] == 0x55).all() and (b[offset + m * n:] == 0x55).all(), "wrote outside the codes buffer"
+
+
+@pytest.mark.parametrize("shape", [(2, 3), (4096, 4096)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_tensor_scratch_holds_atomic_max(shape):
+    """The reference atomicMax-es the tensor's max |x| bits into the caller's
+    int32 (fp8_quant.cu:159-234): afterwards it holds those bits when it was
+    zeroed, and max(initial, amax) bits otherwise, which then sets the scale."""
+    x = inputs.randn(shape, torch.bfloat16, seed=11)
+    x32 = x.float().numpy()
+    amax = np.float32(np.abs(x32).max())
+    q = torch.empty(shape, dtype=torch.uint8, device="cuda")
+    scratch = torch.zeros(1, dtype=torch.int32, device="cuda")
+    _tensor_abi(x.cuda(), q, scratch)
+    assert int(scratch.item()) == int(np.array([amax], dtype=np.float32).view(np.int32)[0])
+    preset = np.float32(1000.0)
+    scratch = torch.tensor(np.array([preset], dtype=np.float32).view(np.int32), device="cuda")
+    scale = _tensor_abi(x.cuda(), q, scratch)
+    s_ref = np.float32(preset / np.float32(448.0))
+    assert_f32_bits_equal(scale, np.array([s_ref], dtype=np.float32))
+    assert_codes_equal(q, ofp8.quant_static(x32, float(s_ref), "e4m3"))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("shape", [(200, 264), (129, 136), (1, 8), (300, 1024)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_block_ragged_tiles_vector_path(shape, dtype):
+    """Row and column counts that are not multiples of the 128x128 tile but
+    keep 16-byte rows (the register-resident block kernel, not the scalar one)."""
+    _check(inputs.randn(shape, dtype, seed=shape[0] + shape[1]), "e4m3", "block")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+def test_block_rows_beyond_32bit_tile_offsets(dtype):
+    """Rows so long that 128 of them exceed 2 GiB: the block kernel addresses
+    them with 64-bit pointers instead of 32-bit buffer offsets."""
+    n = (1 << 31) // (128 * (4 if dtype == torch.float32 else 2)) + 128
+    _check(inputs.randn((2, n), dtype, seed=3), "e4m3", "block")
