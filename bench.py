@@ -119,6 +119,15 @@ def _ops(torch, native):
     ops.append(Op("fp8_quant_tensor", "fp8_tensor_bf16_2048x4096", m1 * n1 * 3 + 8, mk1g, tensor_fp8, m1 * n1 * 3,
                   [m1, n1]))
 
+    # Static scale 0.05 on its own (config 5's static mode fuses it into the producers).
+    m1s, n1s = 16384, 4096
+
+    def mk1s():
+        return dict(x=rn(m1s, n1s), q=torch.empty(m1s, n1s, dtype=f8, device=dev))
+
+    ops.append(Op("fp8_quant_static", "fp8_static0.05_bf16_16384x4096", m1s * n1s * 3, mk1s,
+                  lambda b: native.fp8_quant_static_fwd(b["x"], b["q"], 0.05, "e4m3"), m1s * n1s * 3, [m1s, n1s]))
+
     # 2: RMSNorm + residual, [8192, 4096] bf16, eps 1e-5
     m2, n2 = 8192, 4096
     w2 = (1.0 + 0.1 * torch.randn(n2, device=dev, generator=g)).to(bf16)

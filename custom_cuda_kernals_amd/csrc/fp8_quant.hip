@@ -22,13 +22,14 @@
 namespace cck {
 namespace {
 
-// Store VEC fp8 bytes (4 or 8) at byte offset `off` of `q` (VEC-aligned).
+// Store VEC fp8 bytes (4 or 8) at byte offset `off` of `q` (VEC-aligned),
+// as a streaming store.
 template <int VEC>
 __device__ inline void store_codes(uint8_t* q, int64_t off, const uint32_t (&w)[VEC / 4]) {
   if constexpr (VEC == 8) {
-    *reinterpret_cast<u32x2*>(q + off) = (u32x2){w[0], w[1]};
+    st_stream((u32x2){w[0], w[1]}, reinterpret_cast<u32x2*>(q + off));
   } else {
-    *reinterpret_cast<uint32_t*>(q + off) = w[0];
+    st_stream(w[0], reinterpret_cast<uint32_t*>(q + off));
   }
 }
 
@@ -307,13 +308,17 @@ __global__ __launch_bounds__(256) void fp8_tensor_amax(const void* __restrict__ 
 }
 
 // STATIC: scale is `static_scale`; otherwise it derives from *amax_bits and is
-// written to scale_out[0].
+// written to scale_out[0]. VECTOR: CAST_THREADS threads with CAST_UNROLL
+// 16-byte vectors each, loaded before any is converted; measured on MI355X
+// against 256 threads with one vector per grid-stride step and cached code
+// stores: 32.3 vs 35.7 us at [16384, 4096] bf16, 248 vs 338 us at [65536, 8192].
+constexpr int kCastThreads = 512, kCastUnroll = 2;
+
 template <class C, int FMT, bool STATIC, bool VECTOR>
-__global__ __launch_bounds__(256) void fp8_tensor_cast(const void* __restrict__ x,
-                                                       uint8_t* __restrict__ q,
-                                                       float* __restrict__ scale_out,
-                                                       const int32_t* __restrict__ amax_bits,
-                                                       float static_scale, int64_t total) {
+__global__ __launch_bounds__(VECTOR ? kCastThreads : 256) void fp8_tensor_cast(
+    const void* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ scale_out,
+    const int32_t* __restrict__ amax_bits, float static_scale, int64_t total) {
+  constexpr int T = VECTOR ? kCastThreads : 256;
   float s, amax_t = 0.0f;
   if constexpr (STATIC) {
     s = static_scale;
@@ -324,21 +329,31 @@ __global__ __launch_bounds__(256) void fp8_tensor_cast(const void* __restrict__ 
   }
   const float r = 1.0f / s;
   const bool fast_t = fast_path_ok<FMT>(s, r, amax_t);
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   int64_t done = 0;
   if constexpr (VECTOR) {
+    constexpr int U = kCastUnroll;
     const int64_t nvec = total / C::VEC;
     const u32x4* xv = static_cast<const u32x4*>(x);
-    for (int64_t v = tid; v < nvec; v += stride) {
-      const u32x4 raw = ld_stream(xv + v);
-      bool fast = fast_t;
-      if constexpr (STATIC) fast = fast_path_ok<FMT>(s, r, C::absmax_to_float(C::absmax_vec(raw, 0)));
-      quant_vec<C, FMT>(raw, s, r, fast, q, v * C::VEC);
+    for (int64_t b = (int64_t)blockIdx.x * T * U + threadIdx.x; b < nvec; b += (int64_t)gridDim.x * T * U) {
+      u32x4 raw[U];
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        if (b + k * T < nvec) raw[k] = ld_stream(xv + b + k * T);
+      }
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const int64_t v = b + k * T;
+        if (v < nvec) {
+          bool fast = fast_t;
+          if constexpr (STATIC) fast = fast_path_ok<FMT>(s, r, C::absmax_to_float(C::absmax_vec(raw[k], 0)));
+          quant_vec<C, FMT>(raw[k], s, r, fast, q, v * C::VEC);
+        }
+      }
     }
     done = nvec * C::VEC;
   }
-  for (int64_t i = done + tid; i < total; i += stride) {
+  const int64_t stride = (int64_t)gridDim.x * T;
+  for (int64_t i = done + (int64_t)blockIdx.x * T + threadIdx.x; i < total; i += stride) {
     const float v = C::load1(x, i);
     bool fast = fast_t;
     if constexpr (STATIC) fast = fast_path_ok<FMT>(s, r, __builtin_fabsf(v));
@@ -436,10 +451,11 @@ extern "C" int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, fl
       } else {
         fp8_tensor_amax<C, false><<<1, 256, 0, st>>>(x, total, amax_scratch);
       }
-      const unsigned g = flat_grid(total / C::VEC, 256, 2048);
       if (vec_ok) {
-        fp8_tensor_cast<C, FMT, false, true><<<g, 256, 0, st>>>(x, x_fp8, scale, amax_scratch, 0.0f, total);
+        const unsigned g = flat_grid(total / C::VEC, kCastThreads * kCastUnroll, 1 << 20);
+        fp8_tensor_cast<C, FMT, false, true><<<g, kCastThreads, 0, st>>>(x, x_fp8, scale, amax_scratch, 0.0f, total);
       } else {
+        const unsigned g = flat_grid(total / C::VEC, 256, 2048);
         fp8_tensor_cast<C, FMT, false, false><<<g, 256, 0, st>>>(x, x_fp8, scale, amax_scratch, 0.0f, total);
       }
       return launch_status();
@@ -458,10 +474,11 @@ extern "C" int32_t launch_fp8_quant_static_fwd(const void* x, uint8_t* x_fp8, fl
     return with_fp8(fp8_format, [&](auto f) {
       constexpr int FMT = decltype(f)::value;
       const bool vec_ok = host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
-      const unsigned g = flat_grid(total / C::VEC, 256, 8192);
       if (vec_ok) {
-        fp8_tensor_cast<C, FMT, true, true><<<g, 256, 0, st>>>(x, x_fp8, nullptr, nullptr, scale, total);
+        const unsigned g = flat_grid(total / C::VEC, kCastThreads * kCastUnroll, 1 << 20);
+        fp8_tensor_cast<C, FMT, true, true><<<g, kCastThreads, 0, st>>>(x, x_fp8, nullptr, nullptr, scale, total);
       } else {
+        const unsigned g = flat_grid(total / C::VEC, 256, 8192);
         fp8_tensor_cast<C, FMT, true, false><<<g, 256, 0, st>>>(x, x_fp8, nullptr, nullptr, scale, total);
       }
       return launch_status();
