@@ -155,9 +155,10 @@ __global__ __launch_bounds__(256) void fp8_token_generic(const void* __restrict_
 // Block granularity: one workgroup of THREADS per 128x128 tile, tile kept in
 // registers. Vector path needs n % VEC == 0 and aligned pointers. RSRC loads
 // through a buffer resource based at the tile's first element (32-bit
-// offsets: the launcher checks that 128 rows fit in 2 GiB); measured on
-// MI355X against global-pointer loads at 256 threads: 7.6 vs 9.8 us at
-// [2048, 4096] bf16, 35.1 vs 38.0 us at [16384, 4096].
+// offsets: the launcher checks that 128 rows fit in 2 GiB) and codes are
+// stored as streaming stores; measured on MI355X against 256 threads with
+// global-pointer loads and cached stores: 6.55 vs 9.8 us at [2048, 4096]
+// bf16, 35.0 vs 38.0 us at [16384, 4096].
 // ---------------------------------------------------------------------------
 constexpr int kTile = 128;
 
