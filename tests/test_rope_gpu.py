@@ -3,7 +3,8 @@ baselines/rope.py:129-145): bit-exact (products and differences rounded
 separately in fp32, one rounding to the storage type), out-of-place and in
 place. Shapes: the reference's case table (baselines/rope.py:72-100), its
 scalar-fallback head dims (tests/test_rope_kernel.py:59-84) and BASELINE
-config 4 at full size, in place.
+config 4 at full size, in place, plus head dims 256 and 512 so that every
+launch shape of the vector kernel (1 to 32 chunk lanes per token) runs.
 """
 
 from __future__ import annotations
@@ -18,7 +19,9 @@ from tests._parity import bits_equal
 pytestmark = pytest.mark.gpu
 
 CASES = [(4, 128, 12, 12, 64), (2, 2048, 32, 8, 128), (1, 4096, 32, 8, 128), (3, 17, 8, 2, 64),
-         (8, 1, 8, 8, 64), (1, 8192, 8, 8, 64), (0, 128, 8, 8, 64), (1, 1, 1, 1, 64), (2, 32, 4, 1, 16)]
+         (8, 1, 8, 8, 64), (1, 8192, 8, 8, 64), (0, 128, 8, 8, 64), (1, 1, 1, 1, 64), (2, 32, 4, 1, 16),
+         # head_dim 256 / 512: 32 and 16 chunk lanes (one and two tokens per workgroup)
+         (2, 16, 4, 2, 256), (1, 8, 3, 1, 512)]
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
 
 
