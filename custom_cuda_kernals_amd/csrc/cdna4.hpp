@@ -40,8 +40,19 @@ __device__ inline uint32_t pack2_bf16(float lo, float hi) {
   bf16x2 h = __builtin_convertvector((f32x2){lo, hi}, bf16x2);
   return __builtin_bit_cast(uint32_t, h);
 }
+// The fp32 value v itself, opaque to the optimiser. Before an fp32 -> fp16
+// conversion this keeps the fp32 rounding of the expression that produced v:
+// otherwise the compiler may fold a preceding fp32 multiply into
+// v_fma_mixlo_f16, which rounds the exact product once, straight to fp16,
+// where the eager oracle rounds it to fp32 first (the two differ at rare
+// double-rounding ties). No instruction is emitted.
+__device__ inline float keep_f32(float v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 __device__ inline uint32_t pack2_f16(float lo, float hi) {
-  f16x2 h = __builtin_convertvector((f32x2){lo, hi}, f16x2);
+  f16x2 h = __builtin_convertvector((f32x2){keep_f32(lo), keep_f32(hi)}, f16x2);
   return __builtin_bit_cast(uint32_t, h);
 }
 __device__ inline float bf16_lo(uint32_t w) { return bits_f32(w << 16); }
@@ -140,7 +151,7 @@ struct CodecF16 {
     return (u32x4){pack2_f16(f[0], f[1]), pack2_f16(f[2], f[3]), pack2_f16(f[4], f[5]),
                    pack2_f16(f[6], f[7])};
   }
-  __device__ static float round(float v) { return (float)(_Float16)v; }
+  __device__ static float round(float v) { return (float)(_Float16)keep_f32(v); }
   __device__ static void round2(float& a, float& b) {
     const uint32_t w = pack2_f16(a, b);
     a = f16_lo(w);
@@ -149,7 +160,9 @@ struct CodecF16 {
   __device__ static float load1(const void* p, int64_t i) {
     return (float)static_cast<const _Float16*>(p)[i];
   }
-  __device__ static void store1(void* p, int64_t i, float v) { static_cast<_Float16*>(p)[i] = (_Float16)v; }
+  __device__ static void store1(void* p, int64_t i, float v) {
+    static_cast<_Float16*>(p)[i] = (_Float16)keep_f32(v);
+  }
   __device__ static uint32_t absmax_vec(const u32x4& w, uint32_t acc) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc = pk_max_u16(acc, w[i] & 0x7fff7fffu);

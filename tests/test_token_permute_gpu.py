@@ -69,19 +69,31 @@ def test_gather_out_of_range_rows_are_zero():
 
 
 def _check_combine(eo, ui, w):
+    """Bit-exact against the kernel's defined order (fp32 products added in j
+    order onto +0.0, one rounding to the storage type) for every row length,
+    and against torch's sum, which takes the same order when the row length
+    is a multiple of 16. Otherwise torch's tail path adds in another order;
+    two fp32 orders of a k-term sum differ by at most a few fp32 ulps of
+    sum_j |w_j x_j|, so there the bound is one storage ulp of that magnitude
+    (not of the result, which cancellation can make arbitrarily small)."""
     out = token_combine(eo.cuda(), ui.cuda(), w.cuda()).cpu()
     ref = moe.token_combine(eo, ui, w)
     assert out.shape == ref.shape and out.dtype == eo.dtype
     if out.numel() == 0:
         return None
+    assert bits_equal(out, moe.combine_sequential(eo, ui, w)).all(), "kernel differs from the j-order sum"
     if eo.shape[1] % 16 == 0:
         assert bits_equal(out, ref).all()
-        assert bits_equal(out, moe.combine_sequential(eo, ui, w)).all()
         return 1.0
-    if eo.dtype == torch.float32:
-        torch.testing.assert_close(out, ref, rtol=1e-6, atol=1e-6)
-        return None
-    return assert_ulp_close(out, ref, "combine")["bit_exact_fraction"]
+    # |sum_A - sum_B| <= 2 (k - 1) 2^-24 mag for two fp32 orders (k <= 8 here), plus
+    # at most one storage ulp of the result (|result| <= mag) when the two
+    # straddle a rounding boundary.
+    mag = (eo.float()[ui].abs() * w.abs().unsqueeze(-1)).sum(dim=1).double()
+    ulp = {torch.float32: 0.0, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[eo.dtype]
+    diff = (out.double() - ref.double()).abs()
+    bound = (ulp + 2.0 ** -19) * mag + 1e-30
+    assert bool((diff <= bound).all()), f"max diff / magnitude {float((diff / mag.clamp_min(1e-30)).max())}"
+    return float(bits_equal(out, ref).mean())
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
