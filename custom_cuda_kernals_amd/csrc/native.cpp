@@ -43,6 +43,16 @@ const char* tag_debug(int32_t t) {
   }
 }
 
+const char* tag_to_dtype_str(int32_t t) {
+  switch (t) {
+    case F32: return "torch.float32";
+    case F16: return "torch.float16";
+    case BF16: return "torch.bfloat16";
+    case F8E4M3: return "torch.float8_e4m3fn";
+    default: return "torch.float8_e5m2";
+  }
+}
+
 std::optional<int32_t> tag_from_dtype_str(const std::string& s) {
   if (s == "torch.float32") return F32;
   if (s == "torch.float16") return F16;
@@ -80,6 +90,28 @@ struct View {
   std::vector<int64_t> shape;
 };
 
+// Python objects looked up once per process (the GIL is held in every bound
+// function). They are never released: destroying them after the interpreter
+// has shut down would be unsafe.
+struct PyCache {
+  py::object dtypes[5];  // torch.float32 .. torch.float8_e5m2, indexed by tag
+  py::object raw_stream;  // torch._C._cuda_getCurrentRawStream, or None
+  py::object current_stream;  // torch.cuda.current_stream
+};
+
+const PyCache& py_cache() {
+  static PyCache* c = [] {
+    auto* p = new PyCache;
+    py::module_ torch = py::module_::import("torch");
+    const char* names[5] = {"float32", "float16", "bfloat16", "float8_e4m3fn", "float8_e5m2"};
+    for (int i = 0; i < 5; ++i) p->dtypes[i] = torch.attr(names[i]);
+    p->raw_stream = py::getattr(torch.attr("_C"), "_cuda_getCurrentRawStream", py::none());
+    p->current_stream = torch.attr("cuda").attr("current_stream");
+    return p;
+  }();
+  return *c;
+}
+
 RawView validate_and_extract(const char* name, const py::handle& obj) {
   py::object device = obj.attr("device");
   const std::string device_type = py::str(device.attr("type"));
@@ -91,10 +123,22 @@ RawView validate_and_extract(const char* name, const py::handle& obj) {
     value_error(std::string("argument '") + name + "' must be contiguous");
   }
   RawView v;
-  v.dtype_str = py::str(obj.attr("dtype"));
+  py::object dtype = obj.attr("dtype");
+  const PyCache& cache = py_cache();
+  for (int i = 0; i < 5 && v.dtype_str.empty(); ++i) {
+    if (dtype.is(cache.dtypes[i])) v.dtype_str = tag_to_dtype_str(i);
+  }
+  if (v.dtype_str.empty()) v.dtype_str = py::str(dtype);
   v.ptr = obj.attr("data_ptr")().cast<uintptr_t>();
   v.device_index = device.attr("index").cast<int64_t>();
-  for (py::handle d : obj.attr("shape")) v.shape.push_back(d.cast<int64_t>());
+  py::object shape = obj.attr("shape");
+  if (PyTuple_Check(shape.ptr())) {  // torch.Size is a tuple
+    const Py_ssize_t n = PyTuple_GET_SIZE(shape.ptr());
+    v.shape.reserve((size_t)n);
+    for (Py_ssize_t i = 0; i < n; ++i) v.shape.push_back(py::handle(PyTuple_GET_ITEM(shape.ptr(), i)).cast<int64_t>());
+  } else {
+    for (py::handle d : shape) v.shape.push_back(d.cast<int64_t>());
+  }
   return v;
 }
 
@@ -120,9 +164,15 @@ void check_dtype_matches(const char* name, const View& v, const View& expected, 
   }
 }
 
+// torch.cuda.current_stream(device_index).cuda_stream, read through torch's
+// raw-stream accessor when this torch has it (same value, without building a
+// Stream object).
 void* current_stream(int64_t device_index) {
-  py::object torch = py::module_::import("torch");
-  py::object stream = torch.attr("cuda").attr("current_stream")(device_index);
+  const PyCache& cache = py_cache();
+  if (!cache.raw_stream.is_none()) {
+    return reinterpret_cast<void*>(cache.raw_stream(device_index).cast<uintptr_t>());
+  }
+  py::object stream = cache.current_stream(device_index);
   return reinterpret_cast<void*>(stream.attr("cuda_stream").cast<uintptr_t>());
 }
 
