@@ -195,25 +195,49 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
   }
 }
 
-// Any alignment / row length: scalar accesses; residual_out is re-read by the
-// thread that wrote it.
+// Any alignment / row length: scalar accesses. The sum of squares follows
+// canonical_row_sum's order exactly (vector v = elements [v*VEC, v*VEC + VEC)
+// of the row, zero-padded past its end; vectors 64g .. 64g + 63 form group g,
+// reduced by the same wave64 tree; groups added in index order), so this path
+// gives the same bits as the register-resident kernel for any alignment or
+// row length. Wave w reduces groups w, w + 4, ...; the four group sums of a
+// round are added in order through LDS. residual_out is re-read after the
+// rounds' barriers, by other threads than the ones that wrote it.
 template <class C, int MODE, int FMT>
 __global__ __launch_bounds__(256) void rmsnorm_generic(
     const void* __restrict__ x, const void* __restrict__ res, const void* __restrict__ w,
     void* __restrict__ y, uint8_t* __restrict__ yq, float* __restrict__ scale,
     void* __restrict__ ro, int64_t rows, int64_t cols, float eps, float static_scale) {
+  constexpr int VEC = C::VEC;
   __shared__ uint32_t lds[2 * 4];
+  __shared__ float group_sum[4];
   int parity = 0;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t nvec = (cols + VEC - 1) / VEC;
+  const int64_t ngroups = (nvec + 63) / 64;
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const int64_t base = row * cols;
-    float acc = 0.0f;
-    for (int64_t j = threadIdx.x; j < cols; j += 256) {
-      const float o = C::round(C::load1(x, base + j) + C::load1(res, base + j));
-      C::store1(ro, base + j, o);
-      acc += o * o;
+    float total = 0.0f;
+    for (int64_t g0 = 0; g0 < ngroups; g0 += 4) {
+      const int64_t v = (g0 + wave) * 64 + lane;
+      float part = 0.0f;
+      if (v < nvec) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          const int64_t j = v * VEC + i;
+          if (j < cols) {
+            const float o = C::round(C::load1(x, base + j) + C::load1(res, base + j));
+            C::store1(ro, base + j, o);
+            part += o * o;
+          }
+        }
+      }
+      const float gs = bits_f32(wave_allreduce(f32_bits(part), AddF32{}));
+      if (lane == 0) group_sum[wave] = gs;
+      __syncthreads();
+      for (int i = 0; i < 4 && g0 + i < ngroups; ++i) total += group_sum[i];
+      __syncthreads();
     }
-    const float total = bits_f32(block_allreduce<4>(f32_bits(acc), AddF32{}, lds, parity));
-    parity ^= 1;
     const float inv = 1.0f / __builtin_sqrtf(total / (float)cols + eps);
     if constexpr (MODE == 0) {
       for (int64_t j = threadIdx.x; j < cols; j += 256) {
