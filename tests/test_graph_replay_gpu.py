@@ -1,0 +1,153 @@
+"""Every op captured in a HIP graph (torch.cuda.CUDAGraph) through the
+binding, with preallocated buffers, then replayed: before each replay new
+inputs are copied into the captured input buffers and the outputs are
+overwritten with garbage by eager work, and every replay must reproduce the
+eager launch on the same inputs bit for bit. The per-tensor FP8 op clears
+its amax scratch with torch's zero_() inside the graph (a fill kernel; the
+library itself issues no memset). Three input sets, two rounds of replays.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from custom_cuda_kernals_amd import _native as native
+from oracle import inputs
+
+pytestmark = pytest.mark.gpu
+
+BF16, F8 = torch.bfloat16, torch.float8_e4m3fn
+
+
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    t = t.detach()
+    return t.view(torch.uint8) if t.element_size() == 1 else t.view(torch.int16) if t.element_size() == 2 else t.view(
+        torch.int32) if t.element_size() == 4 else t.view(torch.int64)
+
+
+def _poison(t: torch.Tensor) -> None:
+    _bits(t).fill_(0x5A)
+
+
+def _replay_matches_eager(ins, outs, launch, input_sets):
+    """ins / outs: device tensors the launch reads / writes; input_sets: lists
+    of CPU tensors matching ins."""
+    refs = []
+    for cpu_in in input_sets:
+        for d, c in zip(ins, cpu_in):
+            d.copy_(c)
+        for o in outs:
+            _poison(o)
+        launch()
+        torch.cuda.synchronize()
+        refs.append([_bits(o).clone() for o in outs])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch()
+    torch.cuda.synchronize()
+    for _ in range(2):
+        for cpu_in, ref in zip(input_sets, refs):
+            for d, c in zip(ins, cpu_in):
+                d.copy_(c)
+            for o in outs:
+                _poison(o)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            for o, r in zip(outs, ref):
+                assert torch.equal(_bits(o), r), "graph replay differs from the eager launch"
+
+
+def test_rmsnorm_residual_graph():
+    m, n = 64, 4096
+    sets = [list(inputs.rmsnorm_inputs(m, n, BF16, seed=s)) for s in range(3)]
+    x, r, w = [t.cuda() for t in sets[0]]
+    y, ro = torch.empty_like(x), torch.empty_like(x)
+    _replay_matches_eager([x, r, w], [y, ro], lambda: native.rmsnorm_residual_fwd(x, r, w, y, ro, 1e-5), sets)
+
+
+@pytest.mark.parametrize("static", [None, 0.05])
+def test_rmsnorm_residual_fp8_graph(static):
+    m, n = 64, 4096
+    sets = [list(inputs.rmsnorm_inputs(m, n, BF16, seed=s)) for s in range(3)]
+    x, r, w = [t.cuda() for t in sets[0]]
+    q, ro = torch.empty(m, n, dtype=F8, device="cuda"), torch.empty_like(x)
+    s = torch.empty(m, device="cuda")
+    outs = [q, ro] + ([s] if static is None else [])
+    _replay_matches_eager([x, r, w], outs, lambda: native.rmsnorm_residual_fp8_fwd(
+        x, r, w, q, s if static is None else None, ro, 1e-5, "e4m3", static), sets)
+
+
+def test_swiglu_graph():
+    sets = [list(inputs.swiglu_inputs(32, 14336, BF16, seed=s)) for s in range(3)]
+    g, u = [t.cuda() for t in sets[0]]
+    y = torch.empty_like(g)
+    _replay_matches_eager([g, u], [y], lambda: native.swiglu_fwd(g, u, y), sets)
+
+
+@pytest.mark.parametrize("static", [None, 0.05])
+def test_swiglu_fp8_graph(static):
+    m, n = 32, 14336
+    sets = [list(inputs.swiglu_inputs(m, n, BF16, seed=s)) for s in range(3)]
+    g, u = [t.cuda() for t in sets[0]]
+    q, s = torch.empty(m, n, dtype=F8, device="cuda"), torch.empty(m, device="cuda")
+    outs = [q] + ([s] if static is None else [])
+    _replay_matches_eager([g, u], outs, lambda: native.swiglu_fp8_fwd(g, u, q, s if static is None else None, "e4m3",
+                                                                      static), sets)
+
+
+def test_rope_in_place_graph():
+    sets = []
+    for s in range(3):
+        q, k, cos, sin = inputs.rope_inputs(2, 64, 32, 8, 128, dtype=BF16, seed=s, theta=500000.0)
+        sets.append([q, k, cos, sin])
+    q, k, cos, sin = [t.cuda() for t in sets[0]]
+    _replay_matches_eager([q, k, cos, sin], [q, k], lambda: native.rope_fwd(q, k, cos, sin, q, k), sets)
+
+
+@pytest.mark.parametrize("gran", ["token", "block", "tensor", "static"])
+def test_fp8_quant_graph(gran):
+    m, n = 256, 4096
+    sets = [[inputs.fp8_token_input(m, n, BF16, seed=s)] for s in range(3)]
+    x = sets[0][0].cuda()
+    q = torch.empty(m, n, dtype=F8, device="cuda")
+    if gran == "token":
+        s = torch.empty(m, device="cuda")
+        launch, outs = (lambda: native.fp8_quant_token_fwd(x, q, s, "e4m3")), [q, s]
+    elif gran == "block":
+        s = torch.empty(m // 128, n // 128, device="cuda")
+        launch, outs = (lambda: native.fp8_quant_block_fwd(x, q, s, "e4m3")), [q, s]
+    elif gran == "tensor":
+        s = torch.empty(1, device="cuda")
+        amax = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+        def launch():
+            amax.zero_()
+            native.fp8_quant_tensor_fwd(x, q, s, amax, "e4m3")
+
+        outs = [q, s, amax]
+    else:
+        launch, outs = (lambda: native.fp8_quant_static_fwd(x, q, 0.05, "e4m3")), [q]
+    _replay_matches_eager([x], outs, launch, sets)
+
+
+def test_moe_ops_graph():
+    sets_g = [list(inputs.gather_inputs(512, 1024, 4096, BF16, seed=s)) for s in range(3)]
+    src, idx = [t.cuda() for t in sets_g[0]]
+    dst = torch.empty(1024, 4096, dtype=BF16, device="cuda")
+    _replay_matches_eager([src, idx], [dst], lambda: native.token_gather_fwd(src, idx, dst), sets_g)
+    sets_c = [list(inputs.combine_inputs(256, 6, 4096, BF16, seed=s)) for s in range(3)]
+    eo, ui, w = [t.cuda() for t in sets_c[0]]
+    out = torch.empty(256, 4096, dtype=BF16, device="cuda")
+    _replay_matches_eager([eo, ui, w], [out], lambda: native.token_combine_fwd(eo, ui, w, out), sets_c)
+    sets_r = [[inputs.router_inputs(512, 160, torch.float32, seed=s)] for s in range(3)]
+    lg = sets_r[0][0].cuda()
+    tw, ti = torch.empty(512, 6, device="cuda"), torch.empty(512, 6, dtype=torch.int64, device="cuda")
+    _replay_matches_eager([lg], [tw, ti], lambda: native.moe_router_fwd(lg, tw, ti, True), sets_r)
