@@ -1,0 +1,95 @@
+"""The binding launches on torch.cuda.current_stream() of the tensors' device
+(reference src/kernels/rmsnorm_residual.rs:87-94), so a launch is ordered
+after earlier work on that stream only. Each case runs on a side stream that
+first spins (torch.cuda._sleep, a bounded busy-wait kernel) and then writes
+the real inputs over zeros: a launch issued on any other stream would run
+during the spin and read the zeros. Multi-kernel ops (per-tensor FP8) must
+keep all their kernels on that stream.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from custom_cuda_kernals_amd.kernels import fp8_quant, moe_router, rmsnorm_residual, swiglu_fp8, token_combine
+from oracle import inputs
+
+pytestmark = pytest.mark.gpu
+
+SPIN_CYCLES = 20_000_000  # ~10 ms
+
+
+def _on_side_stream(fill_pairs, op):
+    """fill_pairs: (device tensor, device values) written on the side stream
+    after the spin; op() runs there too. Returns op's outputs after the side
+    stream has drained."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        torch.cuda._sleep(SPIN_CYCLES)
+        for dst, val in fill_pairs:
+            dst.copy_(val)
+        out = op()
+    # Control: work on the default stream runs during the spin and still sees
+    # the zeros, which is what a launch on the wrong stream would read. When
+    # the runtime has put both streams on one hardware queue (there are only
+    # GPU_MAX_HW_QUEUES of them) they run in order and the case cannot
+    # discriminate; tests/test_graph_replay_gpu.py checks the same property
+    # deterministically (a launch off the capturing stream is not replayed).
+    probe = fill_pairs[0][0].clone()
+    torch.cuda.synchronize()
+    if bool(probe.any()):
+        pytest.skip("side and default streams were serialised on one hardware queue")
+    return out
+
+
+def _same(a, b):
+    a = a if isinstance(a, (tuple, list)) else (a,)
+    b = b if isinstance(b, (tuple, list)) else (b,)
+    for x, y in zip(a, b):
+        assert torch.equal(x.view(torch.uint8) if x.element_size() == 1 else x, y.view(torch.uint8) if y.element_size() == 1 else y)
+
+
+def test_rmsnorm_follows_current_stream():
+    x, r, w = [t.cuda() for t in inputs.rmsnorm_inputs(64, 4096, torch.bfloat16, seed=1)]
+    ref = rmsnorm_residual(x, r, w, 1e-5)
+    torch.cuda.synchronize()
+    xz, rz = torch.zeros_like(x), torch.zeros_like(r)
+    out = _on_side_stream([(xz, x), (rz, r)], lambda: rmsnorm_residual(xz, rz, w, 1e-5))
+    _same(out, ref)
+
+
+def test_swiglu_fp8_follows_current_stream():
+    g, u = [t.cuda() for t in inputs.swiglu_inputs(16, 14336, torch.bfloat16, seed=2)]
+    ref = swiglu_fp8(g, u)
+    torch.cuda.synchronize()
+    gz, uz = torch.zeros_like(g), torch.zeros_like(u)
+    out = _on_side_stream([(gz, g), (uz, u)], lambda: swiglu_fp8(gz, uz))
+    _same(out, ref)
+
+
+@pytest.mark.parametrize("gran", ["tensor", "block", "token"])
+def test_fp8_quant_follows_current_stream(gran):
+    x = inputs.fp8_token_input(512, 4096, torch.bfloat16, seed=3).cuda()
+    ref = fp8_quant(x, "e4m3", gran)
+    torch.cuda.synchronize()
+    xz = torch.zeros_like(x)
+    out = _on_side_stream([(xz, x)], lambda: fp8_quant(xz, "e4m3", gran))
+    _same(out, ref)
+
+
+def test_combine_follows_current_stream():
+    eo, ui, w = [t.cuda() for t in inputs.combine_inputs(256, 6, 4096, torch.bfloat16, seed=4)]
+    ref = token_combine(eo, ui, w)
+    torch.cuda.synchronize()
+    eoz = torch.zeros_like(eo)
+    _same(_on_side_stream([(eoz, eo)], lambda: token_combine(eoz, ui, w)), ref)
+
+
+def test_router_follows_current_stream():
+    lg = inputs.router_inputs(512, 160, torch.float32, seed=5).cuda()
+    ref = moe_router(lg, 6)
+    torch.cuda.synchronize()
+    lgz = torch.zeros_like(lg)
+    _same(_on_side_stream([(lgz, lg)], lambda: moe_router(lgz, 6)), ref)
