@@ -108,3 +108,23 @@ def test_long_stream_ragged_lengths(n):
     g, u = inputs.swiglu_inputs(1, n, torch.bfloat16, seed=n % 1000)
     stats = _run(g.view(-1), u.view(-1))
     assert stats["bit_exact_fraction"] == 1.0
+
+
+def test_every_f16_gate_and_strided_f32_gates():
+    """All 2^16 fp16 gate patterns and every 4096th fp32 pattern (1 M values
+    spanning every exponent, incl. subnormals, inf and NaN), with up = 1 so
+    y is the rounded SiLU itself: within the ulp bound of the oracle, NaN
+    exactly where the oracle has NaN. fp16 covers the fast-path edge at
+    |g| = 87 that bf16 gates (edge 20) do not reach."""
+    import numpy as np
+
+    g16 = torch.from_numpy(np.arange(1 << 16, dtype=np.uint16).view(np.int16)).view(torch.float16)
+    g32 = torch.from_numpy((np.arange(1 << 20, dtype=np.uint64) * 4096 + 7).astype(np.uint32).view(np.int32)).view(
+        torch.float32)
+    for g in (g16, g32):
+        y = swiglu(g.cuda(), torch.ones_like(g).cuda()).cpu()
+        y_ref = eager.swiglu(g, torch.ones_like(g))
+        nan = torch.isnan(y_ref)
+        assert torch.equal(torch.isnan(y), nan)
+        stats = assert_ulp_close(y[~nan], y_ref[~nan], f"every {g.dtype} gate")
+        print(f"\n{g.dtype} gates vs oracle: {stats}")
