@@ -195,7 +195,7 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
   if (row < rows) load(row);
   if constexpr (TAB) {
     // Pair fill: measured 0.3-1.6 % faster than fill_single in this kernel
-    // on MI355X (and 1.7 % slower in the flat streaming kernels).
+    // on MI355X (and 1.7 % slower in the static-scale flat kernel).
     SiluTableBF16::fill_pairs(tab, threadIdx.x, THREADS);
     __syncthreads();
   }
