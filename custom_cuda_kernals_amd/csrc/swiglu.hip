@@ -160,14 +160,15 @@ __global__ __launch_bounds__(256) void swiglu_fp8_static_scalar(const void* __re
 constexpr bool kRsrcQ = true;
 constexpr int kPolQ = kPolSC1 | kPolNT;
 
-// Per-token FP8 variant, register-resident rows; y is kept as floats (already
+// FP8 variant with register-resident rows; y is kept as floats (already
 // rounded to T) between the amax reduction and the quantisation. TAB (bf16)
 // selects the LDS SiLU table, filled while the first row's loads are in
-// flight. (A static scale needs no row reduction: swiglu_fp8_static_flat.)
-template <class C, int THREADS, int ITEMS, int FMT, bool TAB>
+// flight. STATIC uses static_scale and skips the row reduction; each thread's
+// own max |y| then selects the fast or exact conversion for its vectors.
+template <class C, int THREADS, int ITEMS, int FMT, bool TAB, bool STATIC>
 __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
     const void* __restrict__ gate, const void* __restrict__ up, uint8_t* __restrict__ yq,
-    float* __restrict__ scale, int64_t rows, int64_t cols) {
+    float* __restrict__ scale, float static_scale, int64_t rows, int64_t cols) {
   constexpr int NW = THREADS / 64;
   constexpr int VEC = C::VEC;
   __shared__ uint32_t lds[2 * NW];
@@ -218,11 +219,20 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
         }
       }
     }
-    // amax >= 0 (or NaN), so unsigned max on its bits is the float maximum.
-    amax = bits_f32(block_allreduce<NW>(f32_bits(amax), MaxU32{}, lds, parity));
-    parity ^= 1;
-    const float s = scale_from_amax<FMT>(amax);
-    if (threadIdx.x == 0) scale[row] = s;
+    float s;
+    if constexpr (STATIC) {
+      // A scheduling fence where the reduction would be: without it the
+      // compiler interleaves the conversion with the SiLU and needs 96 VGPRs
+      // (one 1024-thread workgroup per CU instead of two).
+      __builtin_amdgcn_sched_barrier(0);
+      s = static_scale;
+    } else {
+      // amax >= 0 (or NaN), so unsigned max on its bits is the float maximum.
+      amax = bits_f32(block_allreduce<NW>(f32_bits(amax), MaxU32{}, lds, parity));
+      parity ^= 1;
+      s = scale_from_amax<FMT>(amax);
+      if (threadIdx.x == 0) scale[row] = s;
+    }
     const float r = 1.0f / s;
     const bool fast = fast_path_ok<FMT>(s, r, amax);
     const RowBuf<kRsrcQ, kPolQ> bq(yq + row * cols, (uint32_t)cols);
@@ -276,26 +286,42 @@ __global__ __launch_bounds__(256) void swiglu_fp8_generic(
   }
 }
 
-template <class C, int FMT>
-int32_t launch_swiglu_fp8_token(const void* gate, const void* up, uint8_t* yq, float* scale, int64_t rows,
-                                int64_t cols, hipStream_t st) {
+// Register-resident rows: one workgroup per row for the row-length buckets
+// below; false (nothing launched) when no bucket holds the row or the
+// buffers are not aligned for 16-byte access. STATIC rows are used only with
+// the bf16 table (1024-thread rows).
+template <class C, int FMT, bool STATIC>
+bool launch_swiglu_fp8_rows(const void* gate, const void* up, uint8_t* yq, float* scale, float static_scale,
+                            int64_t rows, int64_t cols, hipStream_t st) {
   const bool vec_ok = (cols % C::VEC == 0) && host_aligned(gate, 16) && host_aligned(up, 16) &&
                       host_aligned(yq, C::VEC);
   const int64_t nvec = cols / C::VEC;
   const unsigned g = row_grid(rows);
+  bool launched = false;
   auto run = [&](auto shape) {
     using S = decltype(shape);
     // The table pays for its per-workgroup fill only on long rows.
     constexpr bool kTab = std::is_same_v<C, CodecBF16> && S::kThreads == 1024;
-    swiglu_fp8_resident<C, S::kThreads, S::kItems, FMT, kTab><<<g, S::kThreads, 0, st>>>(gate, up, yq, scale,
-                                                                                          rows, cols);
+    if constexpr (!STATIC || kTab) {
+      swiglu_fp8_resident<C, S::kThreads, S::kItems, FMT, kTab, STATIC><<<g, S::kThreads, 0, st>>>(
+          gate, up, yq, scale, static_scale, rows, cols);
+      launched = true;
+    }
   };
   // At most two vectors per thread keeps the kernel under 64 VGPRs of row
   // state; 1024-thread rows measured fastest on MI355X at cols = 14336 bf16.
-  const bool done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
-                                             RowShape<512, 2>, RowShape<1024, 2>, RowShape<1024, 4>>(nvec, run);
-  if (!done) {
-    swiglu_fp8_generic<C, FMT><<<g, 256, 0, st>>>(gate, up, yq, scale, rows, cols);
+  if (vec_ok) {
+    pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>, RowShape<512, 2>,
+                   RowShape<1024, 2>, RowShape<1024, 4>>(nvec, run);
+  }
+  return launched;
+}
+
+template <class C, int FMT>
+int32_t launch_swiglu_fp8_token(const void* gate, const void* up, uint8_t* yq, float* scale, int64_t rows,
+                                int64_t cols, hipStream_t st) {
+  if (!launch_swiglu_fp8_rows<C, FMT, false>(gate, up, yq, scale, 0.0f, rows, cols, st)) {
+    swiglu_fp8_generic<C, FMT><<<row_grid(rows), 256, 0, st>>>(gate, up, yq, scale, rows, cols);
   }
   return launch_status();
 }
@@ -352,7 +378,10 @@ extern "C" int32_t launch_swiglu_fp8_fwd(const void* gate, const void* up, uint8
     return with_fp8(fp8_format, [&](auto f) {
       constexpr int FMT = decltype(f)::value;
       if (scale_mode == 0) return launch_swiglu_fp8_token<C, FMT>(gate, up, y_fp8, scale, rows, cols, st);
-      // Static scale: one flat stream over rows * cols elements.
+      if (launch_swiglu_fp8_rows<C, FMT, true>(gate, up, y_fp8, nullptr, static_scale, rows, cols, st)) {
+        return launch_status();
+      }
+      // Otherwise one flat stream over rows * cols elements.
       const int64_t n = rows * cols;
       int64_t done = 0;
       if (host_aligned(gate, 16) && host_aligned(up, 16) && host_aligned(y_fp8, C::VEC)) {
