@@ -225,3 +225,22 @@ def test_block_rows_beyond_32bit_tile_offsets(dtype):
     them with 64-bit pointers instead of 32-bit buffer offsets."""
     n = (1 << 31) // (128 * (4 if dtype == torch.float32 else 2)) + 128
     _check(inputs.randn((2, n), dtype, seed=3), "e4m3", "block")
+
+
+def test_block_scales_keep_a_small_tile_resolved_next_to_an_outlier_tile():
+    """The kernels' block and tensor outputs, dequantised with the library's
+    own fp8_format.dequantize: the small tile next to an outlier tile keeps a
+    smaller error under 128x128 scales (as the oracle test of the same name)."""
+    from custom_cuda_kernals_amd.fp8_format import dequantize
+
+    g = torch.Generator().manual_seed(11)
+    x = torch.zeros(256, 256)
+    x[:128, :128] = torch.randn(128, 128, generator=g) * 0.01
+    x[128:, 128:] = torch.randn(128, 128, generator=g) * 100.0
+    xd = x.cuda()
+    errs = {}
+    for gran in ("tensor", "block"):
+        q, s = fp8_quant(xd, "e4m3", gran)
+        deq = dequantize(q, s, gran).cpu()
+        errs[gran] = float((deq[:128, :128] - x[:128, :128]).abs().mean())
+    assert errs["block"] * 2 < errs["tensor"], errs
