@@ -161,23 +161,29 @@ __global__ __launch_bounds__(256) void fp8_token_generic(const void* __restrict_
 // bf16, 35.0 vs 38.0 us at [16384, 4096].
 // ---------------------------------------------------------------------------
 constexpr int kTile = 128;
+constexpr int64_t kBlockPairMinTiles = 16384;
 
-template <class C, int FMT, int THREADS, bool RSRC>
-__global__ __launch_bounds__(THREADS) void fp8_block_resident(const void* __restrict__ x,
-                                                              uint8_t* __restrict__ q,
-                                                              float* __restrict__ scale, int64_t m,
-                                                              int64_t n) {
+template <class C, int FMT, int THREADS, bool RSRC, int TW>
+__global__ __launch_bounds__(THREADS * TW) void fp8_block_resident(const void* __restrict__ x,
+                                                                   uint8_t* __restrict__ q,
+                                                                   float* __restrict__ scale, int64_t m,
+                                                                   int64_t n) {
   constexpr int VPR = kTile / C::VEC;  // vectors per tile row
   constexpr int RPP = THREADS / VPR;   // tile rows per pass
   constexpr int ITEMS = kTile / RPP;
-  constexpr int NW = THREADS / 64;
-  __shared__ uint32_t lds[2 * NW];
-  const int cv = threadIdx.x % VPR;
-  const int rr = threadIdx.x / VPR;
-  const int64_t origin = (int64_t)blockIdx.y * kTile * n + (int64_t)blockIdx.x * kTile;
-  const int64_t col = (int64_t)blockIdx.x * kTile + cv * C::VEC;
+  constexpr int NW = THREADS / 64;     // waves per tile
+  __shared__ uint32_t lds[2 * NW * TW];
+  const int tile = TW == 1 ? 0 : (int)(threadIdx.x / THREADS);  // which of the workgroup's tiles
+  const int t = TW == 1 ? (int)threadIdx.x : (int)(threadIdx.x % THREADS);
+  const int cv = t % VPR;
+  const int rr = t / VPR;
+  const int64_t tiles_x = (n + kTile - 1) / kTile;
+  const int64_t tx = (int64_t)blockIdx.x * TW + tile;
+  // The workgroup's first element; its TW tiles sit side by side from there.
+  const int64_t origin = (int64_t)blockIdx.y * kTile * n + (int64_t)blockIdx.x * TW * kTile;
+  const int64_t col = tx * kTile + cv * C::VEC;
   const int64_t row0 = (int64_t)blockIdx.y * kTile + rr;
-  const bool col_ok = col < n;
+  const bool col_ok = tx < tiles_x && col < n;
   const int64_t left = (m * n - origin) * C::kBytes;
   const RowBuf<true> bx(static_cast<const char*>(x) + origin * C::kBytes,
                         (uint32_t)(left < 0x7fffffff ? left : 0x7fffffff));
@@ -188,18 +194,28 @@ __global__ __launch_bounds__(THREADS) void fp8_block_resident(const void* __rest
     const int64_t row = row0 + k * RPP;
     if (col_ok && row < m) {
       if constexpr (RSRC) {
-        raw[k] = bx.ld16((uint32_t)(((int64_t)(rr + k * RPP) * n + cv * C::VEC) * C::kBytes));
+        raw[k] = bx.ld16((uint32_t)(((int64_t)(rr + k * RPP) * n + tile * kTile + cv * C::VEC) * C::kBytes));
       } else {
         raw[k] = ld_stream(reinterpret_cast<const u32x4*>(static_cast<const char*>(x) + (row * n + col) * C::kBytes));
       }
       acc = C::absmax_vec(raw[k], acc);
     }
   }
-  acc = block_allreduce<NW>(acc, typename AmaxOp<C>::type{}, lds, 0);
+  if constexpr (TW == 1) {
+    acc = block_allreduce<NW>(acc, typename AmaxOp<C>::type{}, lds, 0);
+  } else {
+    // One LDS slot per wave; each tile combines its own NW waves.
+    acc = wave_allreduce(acc, typename AmaxOp<C>::type{});
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    acc = lds[tile * NW];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) acc = typename AmaxOp<C>::type{}(acc, lds[tile * NW + i]);
+  }
   const float amax = C::absmax_to_float(acc);
   const float s = scale_from_amax<FMT>(amax);
   const float r = 1.0f / s;
-  if (threadIdx.x == 0) scale[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = s;
+  if (t == 0 && tx < tiles_x) scale[(int64_t)blockIdx.y * tiles_x + tx] = s;
   const bool fast = fast_path_ok<FMT>(s, r, amax);
 #pragma unroll
   for (int k = 0; k < ITEMS; ++k) {
@@ -411,10 +427,17 @@ extern "C" int32_t launch_fp8_quant_block_fwd(const void* x, uint8_t* x_fp8, flo
     return with_fp8(fp8_format, [&](auto f) {
       constexpr int FMT = decltype(f)::value;
       const bool vec_ok = (n % C::VEC == 0) && host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
-      if (vec_ok && (int64_t)kTile * n * C::kBytes <= 0x7fffffff) {
-        fp8_block_resident<C, FMT, 512, true><<<grid, 512, 0, st>>>(x, x_fp8, scale, m, n);
+      const bool rsrc_ok = (int64_t)kTile * n * C::kBytes <= 0x7fffffff;
+      if (vec_ok && rsrc_ok && nrb * ncb >= kBlockPairMinTiles) {
+        // Two tiles side by side per 1024-thread workgroup: 128.0 vs 131.0 us at
+        // [32768, 8192] bf16, 254.5 vs 265.1 us at [65536, 8192]; no gain below
+        // 16384 tiles (65.7 vs 66.3 us at [16384, 8192] for one tile).
+        const dim3 grid2((unsigned)((ncb + 1) / 2), (unsigned)nrb);
+        fp8_block_resident<C, FMT, 512, true, 2><<<grid2, 1024, 0, st>>>(x, x_fp8, scale, m, n);
+      } else if (vec_ok && rsrc_ok) {
+        fp8_block_resident<C, FMT, 512, true, 1><<<grid, 512, 0, st>>>(x, x_fp8, scale, m, n);
       } else if (vec_ok) {
-        fp8_block_resident<C, FMT, 512, false><<<grid, 512, 0, st>>>(x, x_fp8, scale, m, n);
+        fp8_block_resident<C, FMT, 512, false, 1><<<grid, 512, 0, st>>>(x, x_fp8, scale, m, n);
       } else {
         fp8_block_generic<C, FMT><<<grid, 256, 0, st>>>(x, x_fp8, scale, m, n);
       }

@@ -244,3 +244,27 @@ def test_block_scales_keep_a_small_tile_resolved_next_to_an_outlier_tile():
         deq = dequantize(q, s, gran).cpu()
         errs[gran] = float((deq[:128, :128] - x[:128, :128]).abs().mean())
     assert errs["block"] * 2 < errs["tensor"], errs
+
+
+def test_block_two_tile_workgroups_on_large_ragged_input():
+    """At >= 16384 tiles the block kernel runs two tiles side by side per
+    workgroup. 131 x 131 tiles with a ragged last row and column of tiles
+    (the last workgroup of each tile row has one tile past the edge): a tile's
+    codes and scale depend only on that tile, so sampled tiles (corners, edges,
+    random) are checked against the oracle, and every scale is checked for
+    finiteness and position."""
+    m, n = 128 * 130 + 17, 128 * 130 + 8
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(m, n, device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
+    q, s = fp8_quant(x, "e4m3", "block")
+    torch.cuda.synchronize()
+    assert tuple(s.shape) == (131, 131) and bool(torch.isfinite(s).all()) and bool((s > 0).all())
+    rng = np.random.default_rng(3)
+    tiles = {(0, 0), (0, 130), (130, 0), (130, 130), (65, 129), (129, 65), (130, 1), (1, 130)}
+    tiles |= {(int(a), int(b)) for a, b in rng.integers(0, 131, size=(24, 2))}
+    for ti, tj in sorted(tiles):
+        r0, c0 = ti * 128, tj * 128
+        xt = x[r0:r0 + 128, c0:c0 + 128].float().cpu().numpy()
+        codes, s_ref = ofp8.quant_tensor(xt, "e4m3")
+        assert_codes_equal(q[r0:r0 + 128, c0:c0 + 128].contiguous(), codes, f"tile {ti},{tj}")
+        assert_f32_bits_equal(s[ti, tj].reshape(1), s_ref, f"scale {ti},{tj}")
