@@ -246,7 +246,8 @@ def test_block_scales_keep_a_small_tile_resolved_next_to_an_outlier_tile():
     assert errs["block"] * 2 < errs["tensor"], errs
 
 
-def test_block_two_tile_workgroups_on_large_ragged_input():
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_block_two_tile_workgroups_on_large_ragged_input(dtype):
     """At >= 16384 tiles the block kernel runs two tiles side by side per
     workgroup. 131 x 131 tiles with a ragged last row and column of tiles
     (the last workgroup of each tile row has one tile past the edge): a tile's
@@ -255,7 +256,7 @@ def test_block_two_tile_workgroups_on_large_ragged_input():
     finiteness and position."""
     m, n = 128 * 130 + 17, 128 * 130 + 8
     g = torch.Generator(device="cuda").manual_seed(5)
-    x = torch.randn(m, n, device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
+    x = torch.randn(m, n, device="cuda", dtype=torch.float32, generator=g).to(dtype)
     q, s = fp8_quant(x, "e4m3", "block")
     torch.cuda.synchronize()
     assert tuple(s.shape) == (131, 131) and bool(torch.isfinite(s).all()) and bool((s > 0).all())
