@@ -141,9 +141,9 @@ extern "C" int32_t launch_rope_fwd(const void* q, const void* k, const void* cos
     if (chunks == 8) {
       CCK_ROPE(8, 1);  // measured fastest on MI355X for head_dim 128 bf16
     } else if (chunks == 4) {
-      CCK_ROPE(4, 8);
+      CCK_ROPE(4, 1);  // bf16 head_dim 64: 64.1 vs 67.8 us for eight tokens per workgroup
     } else if (chunks == 16) {
-      CCK_ROPE(16, 2);
+      CCK_ROPE(16, 1);  // fp32 head_dim 128: 219.7 vs 231.5 us for two tokens per workgroup
     } else if (chunks == 2) {
       CCK_ROPE(2, 16);
     } else if (chunks == 1) {
