@@ -252,3 +252,39 @@ def test_moe_router_checks():
     with pytest.raises(RuntimeError, match=r"k \(9\) must be <= num_experts \(8\)"):
         r(F(4, 8), F(4, 9, dtype=torch.float32), F(4, 9, dtype=i64), True)
     _raises(r, F(4, 300), F(4, 2, dtype=torch.float32), F(4, 2, dtype=i64), True, match="maximum of 256")
+
+
+def test_header_is_plain_c_and_links(tmp_path):
+    """A C99 program (the way cgo, a Rust -sys crate or any C host sees the
+    boundary) includes the header, links libcustom_kernels_amd.so, and gets
+    0 for empty work and 1 for an unknown tag from a few launchers, with no
+    GPU: those paths return before any device call."""
+    import os
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "abi.c"
+    src.write_text(r"""
+#include <stdio.h>
+#include "custom_kernels_amd.h"
+int main(void) {
+  int bad = 0;
+  bad |= launch_rmsnorm_residual_fwd(0, 0, 0, 0, 0, 0, 4096, 1e-5f, CCK_DTYPE_BF16, 0) != 0;
+  bad |= launch_swiglu_fwd(0, 0, 0, 0, CCK_DTYPE_BF16, 0) != 0;
+  bad |= launch_fp8_quant_token_fwd(0, 0, 0, 0, 16, CCK_DTYPE_BF16, CCK_DTYPE_F8E4M3, 0) != 0;
+  bad |= launch_swiglu_fp8_fwd(0, 0, 0, 0, 4, 16, 0.f, 7, CCK_DTYPE_BF16, CCK_DTYPE_F8E4M3, 0) != 1;
+  bad |= launch_moe_router_fwd(0, 0, 0, 4, 300, 2, CCK_DTYPE_F32, 1, 0) != 1;
+  printf("%s\n", bad ? "FAIL" : "OK");
+  return bad;
+}
+""")
+    lib_dir = os.path.dirname(_cck.LIB_PATH)
+    include_dir = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+    exe = tmp_path / "abi"
+    subprocess.run([cc, "-std=c99", "-Wall", "-Werror", f"-I{include_dir}", str(src), f"-L{lib_dir}",
+                    "-lcustom_kernels_amd", f"-Wl,-rpath,{lib_dir}", "-o", str(exe)], check=True)
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert run.returncode == 0 and run.stdout.strip() == "OK", run.stdout + run.stderr
