@@ -368,7 +368,7 @@ def main():
     args = _parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
-                          "(multi-GPU sharding is design-only, see DESIGN.md)"}))
+                          "(the per-GPU kernels shard by token rows with no communication; only one GPU is measured)"}))
         sys.exit(2)
 
     import torch
