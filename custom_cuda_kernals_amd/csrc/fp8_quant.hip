@@ -83,17 +83,31 @@ __global__ __launch_bounds__(THREADS) void fp8_token_resident(const void* __rest
   // Buffer-resource row access (no per-lane 64-bit addressing): 6.6 vs 6.8 us
   // at [2048, 4096] bf16 on MI355X.
   const uint32_t row_bytes = (uint32_t)(cols * C::kBytes);
-  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+  // A row's loads are issued one iteration ahead: the first row's at kernel
+  // entry, before the loop set-up, and each next row's before the current
+  // one is reduced. 6.0 vs 6.3-6.5 us at [2048, 4096] bf16 on MI355X against
+  // loading inside the loop (where each load also waited for the one before
+  // it to feed the max).
+  u32x4 nxt[ITEMS];
+  auto issue = [&](int64_t row) {
     const RowBuf<true> bx(static_cast<const char*>(x) + row * cols * C::kBytes, row_bytes);
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+      const uint32_t v = threadIdx.x + k * THREADS;
+      if (v < (uint32_t)nvec) nxt[k] = bx.ld16(v * 16u);
+    }
+  };
+  if ((int64_t)blockIdx.x < rows) issue(blockIdx.x);
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     u32x4 raw[ITEMS];
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) raw[k] = nxt[k];
+    if (row + gridDim.x < rows) issue(row + gridDim.x);
     uint32_t acc = 0;
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       const uint32_t v = threadIdx.x + k * THREADS;
-      if (v < (uint32_t)nvec) {
-        raw[k] = bx.ld16(v * 16u);
-        acc = C::absmax_vec(raw[k], acc);
-      }
+      if (v < (uint32_t)nvec) acc = C::absmax_vec(raw[k], acc);
     }
     acc = block_allreduce<NW>(acc, typename AmaxOp<C>::type{}, lds, parity);
     parity ^= 1;

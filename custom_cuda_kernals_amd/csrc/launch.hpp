@@ -62,11 +62,15 @@ inline int32_t launch_status() { return (int32_t)hipGetLastError(); }
 
 inline bool host_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Grid size for row-per-workgroup kernels: one workgroup per row up to the
-// grid limit; kernels loop over rows beyond it.
+// Workgroup cap of the row-per-workgroup kernels (rows, tokens, MoE rows):
+// one workgroup per row up to it, and beyond it each workgroup loops over
+// rows blockIdx.x, blockIdx.x + gridDim.x, ... 65536 workgroups fill the
+// 256 CUs many times over, so large inputs lose nothing, and the looping
+// path is reachable at test sizes (a few MB).
+constexpr int64_t kMaxRowGroups = 65536;
+
 inline unsigned row_grid(int64_t rows) {
-  const int64_t cap = 1 << 30;
-  return (unsigned)(rows < cap ? rows : cap);
+  return (unsigned)(rows < kMaxRowGroups ? rows : kMaxRowGroups);
 }
 
 inline unsigned flat_grid(int64_t work_items, int threads, int64_t cap) {

@@ -123,7 +123,7 @@ extern "C" int32_t launch_moe_router_fwd(const void* logits, float* topk_weights
   hipStream_t st = static_cast<hipStream_t>(stream);
   return with_codec(dtype, [&](auto codec) {
     using C = decltype(codec);
-    moe_router_waves<C><<<flat_grid(num_tokens, kWavesPerGroup, int64_t(1) << 30), 256, 0, st>>>(
+    moe_router_waves<C><<<flat_grid(num_tokens, kWavesPerGroup, kMaxRowGroups), 256, 0, st>>>(
         logits, topk_weights, topk_indices, num_tokens, (int)num_experts, (int)k, renormalize != 0);
     return launch_status();
   });

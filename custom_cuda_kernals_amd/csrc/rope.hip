@@ -136,7 +136,7 @@ extern "C" int32_t launch_rope_fwd(const void* q, const void* k, const void* cos
     const int chunks = vec_ok && max_row_bytes <= 0x7fffffff ? half / C::VEC : 0;
     // TOK tokens per workgroup, 256/TOK threads per token, CHUNKS chunk lanes.
 #define CCK_ROPE(CH_, TOK_)                                                                  \
-  rope_tokens<C, CH_, TOK_><<<flat_grid(tokens, TOK_, 1 << 30), 256, 0, st>>>(             \
+  rope_tokens<C, CH_, TOK_><<<flat_grid(tokens, TOK_, kMaxRowGroups), 256, 0, st>>>(       \
       q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d)
     if (chunks == 8) {
       CCK_ROPE(8, 1);  // measured fastest on MI355X for head_dim 128 bf16

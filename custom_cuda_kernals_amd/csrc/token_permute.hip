@@ -175,7 +175,7 @@ int32_t gather(const void* src, const int64_t* indices, void* dst, int64_t n_dst
   if (n_dst <= 0 || h <= 0) return (int32_t)hipSuccess;
   const int32_t es = elem_bytes(dtype);
   if (es == 0) return (int32_t)hipErrorInvalidValue;
-  const unsigned grid = (unsigned)(n_dst < (int64_t(1) << 30) ? n_dst : (int64_t(1) << 30));
+  const unsigned grid = row_grid(n_dst);
   const int64_t row_bytes = h * es;
   if (row_bytes % 16 == 0 && host_aligned(src, 16) && host_aligned(dst, 16)) {
     // One vector per thread, up to 512 threads: measured best on MI355X for
@@ -203,7 +203,7 @@ int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, 
   if (n_tokens <= 0 || k <= 0 || h <= 0) return (int32_t)hipSuccess;
   return with_codec(dtype, [&](auto codec) {
     using C = decltype(codec);
-    const unsigned grid = (unsigned)(n_tokens < (int64_t(1) << 30) ? n_tokens : (int64_t(1) << 30));
+    const unsigned grid = row_grid(n_tokens);
     if (h % C::VEC == 0 && host_aligned(eo, 16) && host_aligned(out, 16)) {
       // Two expert rows in flight per step. Top-1/2 rows: 4 vectors per thread
       // (9.4 us at T=2048, k=2, hidden 4096 bf16); deeper top-k: 2 per thread
