@@ -73,6 +73,13 @@ inline unsigned row_grid(int64_t rows) {
   return (unsigned)(rows < kMaxRowGroups ? rows : kMaxRowGroups);
 }
 
+// Dynamic LDS to reserve per workgroup (the kernel never touches it) so that
+// at most N workgroups are resident on a CU: gfx950 has 160 KB of LDS per
+// CU, and N * bytes <= 160 KB < (N + 1) * bytes. Some streaming kernels run
+// faster with fewer workgroups in flight than their registers allow.
+template <int N>
+constexpr unsigned kLdsForGroupsPerCu = (160u * 1024u * 2u) / (2u * N + 1u);
+
 inline unsigned flat_grid(int64_t work_items, int threads, int64_t cap) {
   int64_t g = (work_items + threads - 1) / threads;
   if (g < 1) g = 1;

@@ -134,22 +134,29 @@ extern "C" int32_t launch_rope_fwd(const void* q, const void* k, const void* cos
                         host_aligned(ct, 16) && host_aligned(sn, 16);
     const int64_t max_row_bytes = (int64_t)(hq > hkv ? hq : hkv) * d * C::kBytes;
     const int chunks = vec_ok && max_row_bytes <= 0x7fffffff ? half / C::VEC : 0;
-    // TOK tokens per workgroup, 256/TOK threads per token, CHUNKS chunk lanes.
-#define CCK_ROPE(CH_, TOK_)                                                                  \
-  rope_tokens<C, CH_, TOK_><<<flat_grid(tokens, TOK_, kMaxRowGroups), 256, 0, st>>>(       \
+    // TOK tokens per workgroup, 256/TOK threads per token, CHUNKS chunk lanes,
+    // LDS_ bytes reserved to cap the workgroups resident per CU.
+#define CCK_ROPE(CH_, TOK_, LDS_)                                                            \
+  rope_tokens<C, CH_, TOK_><<<flat_grid(tokens, TOK_, kMaxRowGroups), 256, LDS_, st>>>(    \
       q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d)
     if (chunks == 8) {
-      CCK_ROPE(8, 1);  // measured fastest on MI355X for head_dim 128 bf16
+      // Measured fastest on MI355X for head_dim 128 bf16, with at most 6
+      // workgroups per CU (8 fit): 102.0 vs 103.8 us at config 4.
+      CCK_ROPE(8, 1, kLdsForGroupsPerCu<6>);
     } else if (chunks == 4) {
-      CCK_ROPE(4, 1);  // bf16 head_dim 64: 64.1 vs 67.8 us for eight tokens per workgroup
+      // bf16 head_dim 64: 64.1 vs 67.8 us for eight tokens per workgroup;
+      // 61.7 vs 64.1 us with at most 6 workgroups per CU.
+      CCK_ROPE(4, 1, kLdsForGroupsPerCu<6>);
     } else if (chunks == 16) {
-      CCK_ROPE(16, 1);  // fp32 head_dim 128: 219.7 vs 231.5 us for two tokens per workgroup
+      // fp32 head_dim 128: 219.7 vs 231.5 us for two tokens per workgroup (a
+      // cap of 5 or 6 workgroups per CU measured no different).
+      CCK_ROPE(16, 1, 0);
     } else if (chunks == 2) {
-      CCK_ROPE(2, 16);
+      CCK_ROPE(2, 16, 0);
     } else if (chunks == 1) {
-      CCK_ROPE(1, 32);
+      CCK_ROPE(1, 32, 0);
     } else if (chunks == 32) {
-      CCK_ROPE(32, 1);
+      CCK_ROPE(32, 1, 0);
     } else {
       const int64_t total = tokens * (int64_t)(hq + hkv) * half;
       rope_scalar<C><<<flat_grid(total, 256, 1 << 20), 256, 0, st>>>(q, k, ct, sn, q_out, k_out,

@@ -352,10 +352,13 @@ extern "C" int32_t launch_swiglu_fwd(const void* gate, const void* up, void* y, 
       u32x4* y4 = static_cast<u32x4*>(y);
       if (nvec > 0) {
         // 512 threads x 2 vectors: 108.9 us at [8192, 14336] bf16 on MI355X,
-        // against 109.8 at 256 x 4 and 111.4-116 for the other shapes tried.
+        // against 109.8 at 256 x 4 and 111.4-116 for the other shapes tried;
+        // at most 3 workgroups per CU (4 fit): 107.3-107.9 vs 108.0-108.5 us
+        // (fp16 107.4 vs 108.4, fp32 216.1 vs 218.4).
         constexpr int THREADS = 512, UNROLL = 2;
         swiglu_flat<C, THREADS, UNROLL>
-            <<<flat_grid((nvec + UNROLL - 1) / UNROLL, THREADS, 1 << 20), THREADS, 0, st>>>(g4, u4, y4, nvec);
+            <<<flat_grid((nvec + UNROLL - 1) / UNROLL, THREADS, 1 << 20), THREADS, kLdsForGroupsPerCu<3>, st>>>(
+                g4, u4, y4, nvec);
       }
       done = nvec * C::VEC;
     }
