@@ -294,7 +294,10 @@ __global__ __launch_bounds__(kPartialThreads) void fp8_tensor_partial(const void
       u32x4 v[U];
 #pragma unroll
       for (int k = 0; k < U; ++k) {
-        if (b + k * T < nvec) v[k] = ld_stream(xv + b + k * T);
+        // Cached loads (not streaming): x is then more often still on chip
+        // when the cast pass reads it again, 54.0 vs 57.0 us for the whole op
+        // at [16384, 4096] bf16 and 13.6 vs 13.7 at [2048, 4096] on MI355X.
+        if (b + k * T < nvec) v[k] = xv[b + k * T];
       }
 #pragma unroll
       for (int k = 0; k < U; ++k) {
@@ -365,7 +368,12 @@ __global__ __launch_bounds__(VECTOR ? kCastThreads : 256) void fp8_tensor_cast(
     constexpr int U = kCastUnroll;
     const int64_t nvec = total / C::VEC;
     const u32x4* xv = static_cast<const u32x4*>(x);
-    for (int64_t b = (int64_t)blockIdx.x * T * U + threadIdx.x; b < nvec; b += (int64_t)gridDim.x * T * U) {
+    // After the partial pass the dynamic-scale cast walks the workgroups'
+    // chunks last-first, so it starts on the most recently read part of x:
+    // 13.3 vs 13.6 us for the whole op at [2048, 4096] bf16 (no change at
+    // [16384, 4096]).
+    const int64_t bid = STATIC ? (int64_t)blockIdx.x : (int64_t)(gridDim.x - 1 - blockIdx.x);
+    for (int64_t b = bid * T * U + threadIdx.x; b < nvec; b += (int64_t)gridDim.x * T * U) {
       u32x4 raw[U];
 #pragma unroll
       for (int k = 0; k < U; ++k) {
