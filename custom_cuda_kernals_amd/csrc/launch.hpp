@@ -79,6 +79,9 @@ inline unsigned row_grid(int64_t rows) {
 // faster with fewer workgroups in flight than their registers allow.
 template <int N>
 constexpr unsigned kLdsForGroupsPerCu = (160u * 1024u * 2u) / (2u * N + 1u);
+static_assert(3 * kLdsForGroupsPerCu<3> <= 160u * 1024u && 4 * kLdsForGroupsPerCu<3> > 160u * 1024u);
+static_assert(6 * kLdsForGroupsPerCu<6> <= 160u * 1024u && 7 * kLdsForGroupsPerCu<6> > 160u * 1024u);
+static_assert(kLdsForGroupsPerCu<3> <= 64u * 1024u);  // within the default per-workgroup limit
 
 inline unsigned flat_grid(int64_t work_items, int threads, int64_t cap) {
   int64_t g = (work_items + threads - 1) / threads;
