@@ -53,6 +53,8 @@ def _parse():
                         "(for counter-collection runs; includes host launch overhead)")
     p.add_argument("--block", action="store_true",
                    help="also time the Llama-3-8B decoder block (eager / fused / fp8) at S=4096")
+    p.add_argument("--no-ceilings", action="store_true",
+                   help="skip the practical-ceiling streams (pure traffic with four config ops' byte patterns)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a 256 MiB device-to-device torch copy, the reference kernel "
                         "for scaling FETCH_SIZE / WRITE_SIZE counters")
@@ -225,7 +227,7 @@ def _ops(torch, native):
     return ops
 
 
-def _time_op(torch, op, steps, warmup, use_graph=True):
+def _time_op(torch, op, steps, warmup, use_graph=True, per_call=True):
     nsets = max(2, math.ceil(ROTATE_BYTES / op.set_bytes))
     sets = [op.make_set() for _ in range(nsets)]
     torch.cuda.synchronize()
@@ -267,12 +269,56 @@ def _time_op(torch, op, steps, warmup, use_graph=True):
     us = ms * 1000.0 / steps
     gbps = op.nbytes / (us * 1e-6) / 1e9
     del graph
-    per_call = _per_call_us(torch, op, sets)
+    per_call = _per_call_us(torch, op, sets) if per_call else None
     del sets
     torch.cuda.empty_cache()
     return {"workload": op.workload, "shape": op.shape, "us": round(us, 3), "GB_per_s": round(gbps, 1),
             "frac_of_8TBps": round(gbps / PEAK_GBPS, 4), "algorithmic_bytes": op.nbytes,
             "steps": steps, "buffer_sets": nsets, "total_ms": round(ms, 4), "per_call": per_call}
+
+
+def _ceilings(torch, steps, warmup):
+    """Practical HBM ceilings on this GPU: pure traffic streams with the byte
+    pattern of four config ops (cck_hbm_stream, csrc/calibrate.hip: 16-byte
+    nontemporal vectors, no arithmetic), timed exactly like the ops. An op's
+    fraction of the 8 TB/s peak reads against its pattern's fraction here."""
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "custom_cuda_kernals_amd", "libcustom_kernels_amd.so"))
+    fn = lib.cck_hbm_stream
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_void_p]
+    u8 = torch.uint8
+    # (name, pattern, op it bounds, vectors per input stream, input streams, output bytes per vector)
+    cases = [
+        ("copy_1r1w", 0, "rope_inplace", 8 * 4096 * 40 * 128 * 2 // 16, 1, 16),
+        ("stream_2r1w", 1, "swiglu", 8192 * 14336 * 2 // 16, 2, 16),
+        ("rows_2r2w_barrier", 2, "rmsnorm_residual", 8192 * 4096 * 2 // 16, 2, 32),
+        ("stream_r16w8", 3, "fp8_quant_token", 2048 * 4096 * 2 // 16, 1, 8),
+    ]
+    out = {}
+    for name, pattern, bounds, nv, reads, wbytes in cases:
+        def make_set(nv=nv, reads=reads, wbytes=wbytes):
+            s = {"a": torch.empty(nv * 16, dtype=u8, device="cuda"),
+                 "c": torch.empty(nv * min(wbytes, 16), dtype=u8, device="cuda")}
+            if reads == 2:
+                s["b"] = torch.empty(nv * 16, dtype=u8, device="cuda")
+            if wbytes == 32:
+                s["d"] = torch.empty(nv * 16, dtype=u8, device="cuda")
+            return s
+
+        def launch(s, pattern=pattern, nv=nv):
+            ptr = lambda k: s[k].data_ptr() if k in s else None
+            rc = fn(pattern, ptr("a"), ptr("b"), ptr("c"), ptr("d"), nv, torch.cuda.current_stream().cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"cck_hbm_stream failed, hipError_t = {rc}")
+
+        nbytes = nv * (16 * reads + wbytes)
+        op = Op(name, f"hbm_{name}", nbytes, make_set, launch, nbytes, None)
+        r = _time_op(torch, op, steps, warmup, per_call=False)
+        out[name] = {"bounds": bounds, "us": r["us"], "GB_per_s": r["GB_per_s"], "frac_of_8TBps": r["frac_of_8TBps"],
+                     "bytes": nbytes}
+    return out
 
 
 def _per_call_us(torch, op, sets, calls=30):
@@ -388,6 +434,14 @@ def main():
             continue
         results[op.name] = _time_op(torch, op, args.steps, args.warmup, use_graph=not args.no_graph)
         print(f"# {op.name}: {results[op.name]}", file=sys.stderr, flush=True)
+    ceilings = None
+    if not args.no_ceilings and not args.no_graph:
+        ceilings = _ceilings(torch, args.steps, args.warmup)
+        for name, c in ceilings.items():
+            done = results.get(c["bounds"])
+            if done:
+                c["op_frac_of_ceiling"] = round(done["GB_per_s"] / c["GB_per_s"], 4)
+            print(f"# ceiling {name}: {c}", file=sys.stderr, flush=True)
     if args.copy_calibration:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -418,6 +472,8 @@ def main():
                      "frac": round(achieved / PEAK_GBPS, 4), "traffic": _traffic(head_name)},
         "ops": results,
     }
+    if ceilings:
+        line["ceilings"] = ceilings
     if args.block:
         line["block"] = _block_latency(torch)
     if not args.no_cpu_baseline:

@@ -24,7 +24,7 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libcustom_kernels_amd.so"
 HIP_SOURCES = ["fp8_quant.hip", "rmsnorm_residual.hip", "swiglu.hip", "rope.hip", "token_permute.hip", "moe_router.hip",
-               "selftest.hip"]
+               "selftest.hip", "calibrate.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [

@@ -179,6 +179,18 @@ int32_t cck_scale_selftest(uint64_t start, uint64_t count, int32_t fp8_format,
  * layout. */
 int32_t cck_silu_table_selftest(unsigned long long* counters, void* stream);
 
+/* HBM calibration stream (no reference counterpart): one launch of a pure
+ * traffic pattern on 16-byte nontemporal vectors, to measure the practical
+ * bandwidth ceiling of the ops' access patterns. n_vec counts the 16-byte
+ * vectors of one input stream. pattern 0: copy a -> c; 1: two reads, one
+ * write (a, b -> c); 2: rows of 512 vectors, two reads and two writes with a
+ * workgroup barrier between the stores (a, b -> c, d; n_vec % 512 == 0);
+ * 3: read 16 bytes, write 8 (a -> c, c holds 8 * n_vec bytes). Unused
+ * pointers may be null. hipErrorInvalidValue for an unknown pattern or a
+ * partial row. */
+int32_t cck_hbm_stream(int32_t pattern, const void* a, const void* b, void* c, void* d, int64_t n_vec,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

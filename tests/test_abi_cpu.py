@@ -63,6 +63,15 @@ def test_empty_work_returns_success_without_device_calls():
     assert lib.launch_moe_router_fwd(None, None, None, 8, 16, 0, 0, 1, None) == 0
 
 
+def test_hbm_stream_rejects_bad_arguments_before_device_calls():
+    lib = _cck.load()
+    assert lib.cck_hbm_stream(0, None, None, None, None, 0, None) == 0
+    assert lib.cck_hbm_stream(7, None, None, None, None, 0, None) == 0  # empty work first
+    assert lib.cck_hbm_stream(7, None, None, None, None, 1024, None) == 1
+    assert lib.cck_hbm_stream(-1, None, None, None, None, 1024, None) == 1
+    assert lib.cck_hbm_stream(2, None, None, None, None, 1000, None) == 1  # partial 512-vector row
+
+
 def test_unknown_tags_return_invalid_value_before_device_calls():
     lib = _cck.load()
     assert lib.launch_rmsnorm_residual_fwd(None, None, None, None, None, 4, 8, 1e-5, 9, None) == 1
