@@ -54,7 +54,7 @@ def _parse():
     p.add_argument("--block", action="store_true",
                    help="also time the Llama-3-8B decoder block (eager / fused / fp8) at S=4096")
     p.add_argument("--no-ceilings", action="store_true",
-                   help="skip the practical-ceiling streams (pure traffic with four config ops' byte patterns)")
+                   help="skip the practical-ceiling streams (pure traffic with six config ops' byte patterns)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a 256 MiB device-to-device torch copy, the reference kernel "
                         "for scaling FETCH_SIZE / WRITE_SIZE counters")
@@ -279,7 +279,7 @@ def _time_op(torch, op, steps, warmup, use_graph=True, per_call=True):
 
 def _ceilings(torch, steps, warmup):
     """Practical HBM ceilings on this GPU: pure traffic streams with the byte
-    pattern of four config ops (cck_hbm_stream, csrc/calibrate.hip: 16-byte
+    pattern of six config ops (cck_hbm_stream, csrc/calibrate.hip: 16-byte
     nontemporal vectors, no arithmetic), timed exactly like the ops. An op's
     fraction of the 8 TB/s peak reads against its pattern's fraction here."""
     import ctypes
@@ -295,6 +295,8 @@ def _ceilings(torch, steps, warmup):
         ("stream_2r1w", 1, "swiglu", 8192 * 14336 * 2 // 16, 2, 16),
         ("rows_2r2w_barrier", 2, "rmsnorm_residual", 8192 * 4096 * 2 // 16, 2, 32),
         ("stream_r16w8", 3, "fp8_quant_token", 2048 * 4096 * 2 // 16, 1, 8),
+        ("rows_2r_w8", 4, "swiglu_fp8_token", 8192 * 14336 * 2 // 16, 2, 8),
+        ("rows_2r_w16_w8", 5, "rmsnorm_residual_fp8_token", 16384 * 4096 * 2 // 16, 2, 24),
     ]
     out = {}
     for name, pattern, bounds, nv, reads, wbytes in cases:
@@ -303,8 +305,8 @@ def _ceilings(torch, steps, warmup):
                  "c": torch.empty(nv * min(wbytes, 16), dtype=u8, device="cuda")}
             if reads == 2:
                 s["b"] = torch.empty(nv * 16, dtype=u8, device="cuda")
-            if wbytes == 32:
-                s["d"] = torch.empty(nv * 16, dtype=u8, device="cuda")
+            if wbytes > 16:
+                s["d"] = torch.empty(nv * (wbytes - 16), dtype=u8, device="cuda")
             return s
 
         def launch(s, pattern=pattern, nv=nv):

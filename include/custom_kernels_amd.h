@@ -185,9 +185,12 @@ int32_t cck_silu_table_selftest(unsigned long long* counters, void* stream);
  * vectors of one input stream. pattern 0: copy a -> c; 1: two reads, one
  * write (a, b -> c); 2: rows of 512 vectors, two reads and two writes with a
  * workgroup barrier between the stores (a, b -> c, d; n_vec % 512 == 0);
- * 3: read 16 bytes, write 8 (a -> c, c holds 8 * n_vec bytes). Unused
- * pointers may be null. hipErrorInvalidValue for an unknown pattern or a
- * partial row. */
+ * 3: read 16 bytes, write 8 (a -> c, c holds 8 * n_vec bytes); 4: rows of
+ * 1792 vectors, two 16-byte reads and one 8-byte write per vector (a, b -> c,
+ * c holds 8 * n_vec bytes; n_vec % 1792 == 0); 5: rows of 512 vectors, two
+ * 16-byte reads, a 16-byte write and an 8-byte write per vector (a, b -> c,
+ * d; d holds 8 * n_vec bytes; n_vec % 512 == 0). Unused pointers may be
+ * null. hipErrorInvalidValue for an unknown pattern or a partial row. */
 int32_t cck_hbm_stream(int32_t pattern, const void* a, const void* b, void* c, void* d, int64_t n_vec,
                        void* stream);
 

@@ -70,6 +70,8 @@ def test_hbm_stream_rejects_bad_arguments_before_device_calls():
     assert lib.cck_hbm_stream(7, None, None, None, None, 1024, None) == 1
     assert lib.cck_hbm_stream(-1, None, None, None, None, 1024, None) == 1
     assert lib.cck_hbm_stream(2, None, None, None, None, 1000, None) == 1  # partial 512-vector row
+    assert lib.cck_hbm_stream(4, None, None, None, None, 1024, None) == 1  # partial 1792-vector row
+    assert lib.cck_hbm_stream(5, None, None, None, None, 1000, None) == 1
 
 
 def test_unknown_tags_return_invalid_value_before_device_calls():
