@@ -18,6 +18,11 @@ The headline `value` is the BASELINE config-2 workload (fused RMSNorm +
 residual, bf16 [8192, 4096]); every other config's op is reported under "ops".
 Achieved bandwidth = algorithmic bytes per launch / average launch duration.
 
+"ceilings" holds the practical ceiling of six config ops' traffic on this
+GPU: pure streams with the same bytes per element and row structure and no
+arithmetic (cck_hbm_stream), timed the same way, with each op's fraction of
+its stream.
+
 The CPU baseline (rank 0, N=1) times the CPU oracle - the torch-CPU
 restatement of the reference's eager op (baselines/rmsnorm_residual.py) - on a
 bounded sample of the same workload on this host's cores.
