@@ -1,0 +1,225 @@
+// Row sums of fp32 addends in the fixed order of PyTorch's CPU float sum over
+// a contiguous last dimension: the order behind the variance
+// `upcast.pow(2).mean(dim=-1)` of the reference's eager RMSNorm
+// (baselines/rmsnorm_residual.py:133), whose last bits reach every output
+// element through rsqrt. Reproducing it makes the kernel's y equal the eager
+// y bit for bit.
+//
+// The order, for a row of n addends:
+//   * vectors of 8 lanes: element e is lane e % 8 of vector V = e / 8, for the
+//     nv = n / 8 whole vectors;
+//   * vector V = 4 i + k is step i of slot k, for i < steps = nv / 4;
+//   * per (slot, lane) the steps fold into acc0 from zero in blocks of 2^P
+//     steps, P = max(4, ceil_log2(steps) / 4); after each whole block
+//     acc1 += acc0; after every 2^P blocks acc2 += acc1 (acc1 = 0), after
+//     every 2^(2P) blocks acc3 += acc2 (acc2 = 0); the steps % 2^P trailing
+//     steps fold into acc0; p = ((acc0 + acc1) + acc2) + acc3;
+//   * the nv % 4 leftover vectors are added to slot 0 in order, then
+//     p0 = ((p0 + p1) + p2) + p3 lane by lane;
+//   * total = ((0 + the n % 8 trailing scalars in order) + p0[0]) + ... + p0[7].
+// Rows under 8 addends are 4 slots of single elements (leftovers into slot 0).
+//
+// On the device a "region" is 64 consecutive vectors (512 addends): with
+// P = 4 that is one whole block, so a region's 16 steps x 4 slots x 8 lanes
+// are 32 independent sequential folds of 16 addends. The addends of a region
+// are staged in LDS as a[64][8] (vector-major), and lane c < 32 of the
+// folding wave (slot c / 8, lane c % 8) reads a[4 j + c / 8][c % 8] =
+// a_flat[32 j + c] for step j: consecutive lanes, consecutive words.
+#pragma once
+
+#include "cdna4.hpp"
+
+namespace cck {
+
+constexpr int kSumLanes = 8;
+constexpr int kRegionVecs = 64;                     // vectors per region
+constexpr int kRegionAddends = kRegionVecs * kSumLanes;
+constexpr int kFoldLanes = 32;                      // 4 slots x 8 lanes
+
+struct AtenSumPlan {
+  int64_t nv;     // whole 8-lane vectors
+  int64_t steps;  // nv / 4
+  int p;          // log2 of the block length in steps
+  int64_t nfull;  // whole blocks
+  int ntrail;     // steps % 2^p
+  int nleft;      // nv % 4
+  int ntail;      // n % 8
+  __device__ explicit AtenSumPlan(int64_t n) {
+    nv = n / kSumLanes;
+    steps = nv / 4;
+    const int cl = steps <= 2 ? 1 : 64 - __builtin_clzll((unsigned long long)(steps - 1));
+    p = cl / 4 > 4 ? cl / 4 : 4;
+    nfull = steps >> p;
+    ntrail = (int)(steps & ((1 << p) - 1));
+    nleft = (int)(nv & 3);
+    ntail = (int)(n & 7);
+  }
+  __device__ bool has_tail() const { return (ntrail | nleft | ntail) != 0; }
+};
+
+__device__ inline float readlane_f32(float v, int lane) {
+  return bits_f32((uint32_t)__builtin_amdgcn_readlane((int)f32_bits(v), lane));
+}
+
+// Bitmask-mode ds_swizzle within 32-lane halves: lane i reads lane i ^ X.
+template <int X>
+__device__ inline float swizzle_xor(float v) {
+  return bits_f32((uint32_t)__builtin_amdgcn_ds_swizzle((int)f32_bits(v), (X << 10) | 0x1f));
+}
+
+// Continue the folds of lanes c < 32 over `nsteps` steps of a staged region.
+__device__ inline float fold_region(const float* a, int nsteps, int c, float acc) {
+  for (int j = 0; j < nsteps; ++j) acc = acc + a[kFoldLanes * j + c];
+  return acc;
+}
+__device__ inline float fold_region16(const float* a, int c) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc = acc + a[kFoldLanes * j + c];
+  return acc;
+}
+
+// The cascade state of the 32 folds (lanes c < 32; every wave keeps a copy).
+struct AtenCascade {
+  float a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  // Add the fold of whole block `b` (0-based) of a row with block exponent p.
+  __device__ void add_block(float f, int64_t b, int p) {
+    a1 = a1 + f;
+    const int64_t done = b + 1;
+    if ((done & ((int64_t(1) << p) - 1)) == 0) {
+      a2 = a2 + a1;
+      a1 = 0.0f;
+      if ((done & ((int64_t(1) << (2 * p)) - 1)) == 0) {
+        a3 = a3 + a2;
+        a2 = 0.0f;
+      }
+    }
+  }
+};
+
+// Tail data of a row, staged by the wave that holds the last region:
+//   [0, 32)  the folds of the trailing steps (acc0);
+//   [32, 56) the squares of the leftover vectors, 8 per vector;
+//   [56, 64) the trailing scalars.
+constexpr int kTailWords = 64;
+
+// Finish the row sum from the cascade state and the staged tail (every lane
+// of the wave must be active; the result is wave-uniform).
+__device__ inline float aten_finish(const AtenSumPlan& pl, const AtenCascade& cs, const float* tail, int lane) {
+  if (pl.nv == 0) {
+    // Scalar rows (n < 8): slots of single elements.
+    const int n = pl.ntail;
+    const int s = n / 4;
+    float p0 = s ? 0.0f + tail[56] : 0.0f;
+    for (int e = 4 * s; e < n; ++e) p0 = p0 + tail[56 + e];
+    for (int k = 1; k < 4; ++k) p0 = p0 + (s ? 0.0f + tail[56 + k] : 0.0f);
+    return 0.0f + p0;
+  }
+  float v = 0.0f;
+  if (lane < kFoldLanes) {
+    const float a0 = pl.ntrail ? tail[lane] : 0.0f;
+    v = ((a0 + cs.a1) + cs.a2) + cs.a3;
+    if (lane < kSumLanes) {
+      for (int i = 0; i < pl.nleft; ++i) v = v + tail[32 + kSumLanes * i + lane];
+    }
+  }
+  // Lanes 0..7: ((slot 0 + slot 1) + slot 2) + slot 3.
+  const float v1 = swizzle_xor<8>(v), v2 = swizzle_xor<16>(v), v3 = swizzle_xor<24>(v);
+  const float p = ((v + v1) + v2) + v3;
+  float t = 0.0f;
+  for (int e = 0; e < pl.ntail; ++e) t = t + tail[56 + e];
+#pragma unroll
+  for (int l = 0; l < kSumLanes; ++l) t = t + readlane_f32(p, l);
+  return t;
+}
+
+// Copy the leftover vectors and trailing scalars that fall in a staged region
+// (first vector `first_vec` of the row) to the tail words.
+__device__ inline void stage_tail_parts(const AtenSumPlan& pl, const float* a, int64_t first_vec, int lane,
+                                        float* tail) {
+  if (lane < kSumLanes * pl.nleft) {
+    const int64_t v = pl.steps * 4 + lane / kSumLanes;
+    if (v >= first_vec && v < first_vec + kRegionVecs) {
+      tail[32 + lane] = a[(v - first_vec) * kSumLanes + lane % kSumLanes];
+    }
+  }
+  if (lane < pl.ntail) {
+    const int64_t e = pl.nv * kSumLanes + lane - first_vec * kSumLanes;
+    if (e >= 0 && e < kRegionAddends) tail[56 + lane] = a[e];
+  }
+}
+
+// Row sum for the register-resident row kernels: thread t holds 16-byte
+// vectors u = t + k * THREADS of the row (VEC addends each), P = 4 (rows of at
+// most 2^23 addends). The kernel hands each vector's squares to item(k, sq)
+// as soon as it has them (zeros past the row), then calls total().
+//   VEC == 8: one 16-byte vector is one 8-lane vector, so item k of wave w
+//     is region w + NW * k whole; the wave stages it in its own 512 floats of
+//     `stage` and folds it at once, without waiting for the other waves;
+//   VEC == 4: two waves share a region, so the row is staged whole in `stage`
+//     (THREADS * ITEMS * 4 floats) and folded behind a barrier.
+// `bsum` holds 2 x NREG x 32 floats and `tail` 2 x 64, alternated by `parity`
+// so a wave running ahead into the next row never overwrites words that a
+// slower wave still reads.
+template <int VEC, int THREADS, int ITEMS>
+struct ResidentRowSum {
+  static constexpr int NW = THREADS / 64;
+  static constexpr int NREG = (THREADS * ITEMS * VEC + kRegionAddends - 1) / kRegionAddends;
+  static constexpr int kStageFloats = VEC == 8 ? NW * kRegionAddends : THREADS * ITEMS * VEC;
+  const AtenSumPlan& pl;
+  float* stage;
+  float* bs;
+  float* tl;
+  int lane, w, nreg;
+  __device__ ResidentRowSum(const AtenSumPlan& plan, float* stage_, float* bsum, float* tail, int parity)
+      : pl(plan), stage(stage_), bs(bsum + parity * NREG * kFoldLanes), tl(tail + parity * kTailWords) {
+    lane = threadIdx.x & 63;
+    w = threadIdx.x >> 6;
+    nreg = (int)pl.nfull + (pl.has_tail() ? 1 : 0);
+  }
+  __device__ void fold_one(const float* a, int reg) {
+    if (reg < pl.nfull) {
+      const float f = fold_region16(a, lane & 31);
+      if (lane < kFoldLanes) bs[reg * kFoldLanes + lane] = f;
+    } else {
+      const float f = fold_region(a, pl.ntrail, lane & 31, 0.0f);
+      if (lane < kFoldLanes) tl[lane] = f;
+      stage_tail_parts(pl, a, (int64_t)reg * kRegionVecs, lane, tl);
+    }
+  }
+  __device__ void item(int k, const float (&sq)[VEC]) {
+    if constexpr (VEC == 8) {
+      const int reg = w + NW * k;
+      if (reg < nreg) {
+        float* a = stage + w * kRegionAddends;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) a[lane * VEC + i] = sq[i];
+        // LDS accesses of one wave complete in order; the wave barriers only
+        // keep the compiler from moving the fold's reads above these writes,
+        // or the next item's writes above the fold's reads.
+        __builtin_amdgcn_wave_barrier();
+        fold_one(a, reg);
+        __builtin_amdgcn_wave_barrier();
+      }
+    } else {
+      const int u = threadIdx.x + k * THREADS;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) stage[u * VEC + i] = sq[i];
+    }
+  }
+  // Wave-uniform row total (all threads of the workgroup must call it).
+  __device__ float total() {
+    if constexpr (VEC != 8) {
+      __syncthreads();
+      for (int reg = w; reg < nreg; reg += NW) fold_one(stage + reg * kRegionAddends, reg);
+    }
+    __syncthreads();
+    AtenCascade cs;
+    if (lane < kFoldLanes) {
+      for (int b = 0; b < pl.nfull; ++b) cs.add_block(bs[b * kFoldLanes + lane], b, 4);
+    }
+    return aten_finish(pl, cs, tl, lane);
+  }
+};
+
+}  // namespace cck

@@ -248,38 +248,6 @@ __device__ inline uint32_t block_allreduce(uint32_t v, Op op, uint32_t* lds, int
   }
 }
 
-// Row sum whose rounding order depends only on the row, not on the workgroup
-// shape: vector v of the row belongs to group v / 64; a group's 64 per-vector
-// partials are combined by the wave64 tree above, and the group sums are added
-// in group order. With v = threadIdx.x + k * THREADS, item k of wave w holds
-// group k * NW + w, so every (THREADS, ITEMS) shape gives identical bits.
-// `lds` holds 2 * NW * ITEMS floats; `parity` alternates as for block_allreduce.
-template <int NW, int ITEMS>
-__device__ inline float canonical_row_sum(const float (&part)[ITEMS], float* lds, int parity) {
-  float s[ITEMS];
-#pragma unroll
-  for (int k = 0; k < ITEMS; ++k) s[k] = bits_f32(wave_allreduce(f32_bits(part[k]), AddF32{}));
-  if constexpr (NW == 1) {
-    float t = s[0];
-#pragma unroll
-    for (int k = 1; k < ITEMS; ++k) t += s[k];
-    return t;
-  } else {
-    constexpr int G = NW * ITEMS;
-    float* slot = lds + parity * G;
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-#pragma unroll
-      for (int k = 0; k < ITEMS; ++k) slot[k * NW + w] = s[k];
-    }
-    __syncthreads();
-    float t = slot[0];
-#pragma unroll
-    for (int g = 1; g < G; ++g) t += slot[g];
-    return t;
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Division by a scale, bit-identical to IEEE fp32 x / s.
 // ---------------------------------------------------------------------------

@@ -4,17 +4,19 @@
 // Semantics follow the eager oracle's rounding points exactly
 // (baselines/rmsnorm_residual.py:123-136):
 //   residual_out = T(x + residual)                       (rounded to storage)
-//   variance     = sum(float(residual_out)^2) / cols     (fp32)
+//   variance     = sum(float(residual_out)^2) / cols     (fp32, in torch-CPU's
+//                                                         summation order)
 //   inv          = 1 / sqrt(variance + eps)              (both correctly rounded)
 //   y            = T( T(float(residual_out) * inv) * weight )
-// The FP8 variant quantises y (as stored in T) per row (dynamic, the
-// baselines/fp8_quant.py:162-178 formula applied per token) or with a static
-// scale, and does not write y itself.
+// so y equals the eager y bit for bit. The FP8 variant quantises y (as stored
+// in T) per row (dynamic, the baselines/fp8_quant.py:162-178 formula applied
+// per token) or with a static scale, and does not write y itself.
 //
 // Design: one workgroup per row; each thread keeps its ITEMS 16-byte vectors
 // of residual_out in registers between the sum-of-squares reduction and the
 // normalisation, so x and residual are read from HBM exactly once and
 // residual_out / y (or the FP8 codes) written once.
+#include "aten_sum.hpp"
 #include "launch.hpp"
 
 namespace cck {
@@ -55,9 +57,14 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
     void* __restrict__ ro, int64_t rows, int64_t cols, float eps, float static_scale) {
   constexpr int NW = THREADS / 64;
   constexpr int VEC = C::VEC;
+  constexpr int NREG = (THREADS * ITEMS * VEC + kRegionAddends - 1) / kRegionAddends;
   __shared__ uint32_t lds[2 * NW];
-  __shared__ float lds_sum[2 * NW * ITEMS];
+  using RowSum = ResidentRowSum<VEC, THREADS, ITEMS>;
+  __shared__ float sum_stage[RowSum::kStageFloats];
+  __shared__ float sum_blocks[2 * NREG * kFoldLanes];
+  __shared__ float sum_tail[2 * kTailWords];
   const int nvec = (int)(cols / VEC);
+  const AtenSumPlan plan(cols);
   const u32x4* wv = static_cast<const u32x4*>(w);
   const uint32_t row_bytes = (uint32_t)(cols * C::kBytes);
   auto load_row = [&](int64_t row, u32x4 (&xa)[ITEMS], u32x4 (&ra)[ITEMS]) {
@@ -116,11 +123,16 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
       load_row(row, xa, ra);
     }
     u32x4 rov[ITEMS];
-    float part[ITEMS];
+    // torch-CPU's summation order, which does not depend on the launch
+    // shape either: the plain and the FP8 variants (different shapes) give
+    // the same residual_out -> y bits.
+    RowSum rs(plan, sum_stage, sum_blocks, sum_tail, parity);
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       const int v = threadIdx.x + k * THREADS;
-      part[k] = 0.0f;
+      float sq[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) sq[i] = 0.0f;
       if (v < nvec) {
         float fx[VEC], fr[VEC], fo[VEC];
         C::unpack(xa[k], fx);
@@ -131,12 +143,11 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
         bro.st16(rov[k], (uint32_t)v * 16u);
         C::unpack(rov[k], fo);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) part[k] += fo[i] * fo[i];
+        for (int i = 0; i < VEC; ++i) sq[i] = fo[i] * fo[i];
       }
+      rs.item(k, sq);
     }
-    // Shape-independent order: the plain and the FP8 variants (which use
-    // different shapes) produce the same residual_out -> y bits.
-    const float total = canonical_row_sum<NW, ITEMS>(part, lds_sum, parity);
+    const float total = rs.total();
     // Dividing by a power of two is exact scaling: the product with its
     // reciprocal is the same correctly rounded quotient, without the IEEE
     // division sequence (the common case; the branch is wave-uniform).
@@ -220,49 +231,88 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
   }
 }
 
-// Any alignment / row length: scalar accesses. The sum of squares follows
-// canonical_row_sum's order exactly (vector v = elements [v*VEC, v*VEC + VEC)
-// of the row, zero-padded past its end; vectors 64g .. 64g + 63 form group g,
-// reduced by the same wave64 tree; groups added in index order), so this path
-// gives the same bits as the register-resident kernel for any alignment or
-// row length. Wave w reduces groups w, w + 4, ...; the four group sums of a
-// round are added in order through LDS. residual_out is re-read after the
-// rounds' barriers, by other threads than the ones that wrote it.
+// Any alignment / row length: scalar accesses, four waves. The sum of squares
+// follows torch-CPU's order exactly (aten_sum.hpp), so this path gives the
+// same bits as the register-resident kernel for any alignment or row length:
+// the row is cut into blocks of 2^P steps (4 * 2^P vectors of 8 addends,
+// one 64-vector region for P = 4); in each round wave w takes block
+// b0 + w, computes and stores residual_out for it, stages its squares one
+// region at a time in LDS and continues the 32 sequential folds over them;
+// after the round's barrier every wave adds the round's block folds to its
+// copy of the cascade in block order. The last block of a row whose length
+// is not whole blocks is its tail (trailing steps, leftover vectors, trailing
+// scalars). residual_out is re-read in the second pass, after the rounds'
+// barriers, by other threads than the ones that wrote it.
 template <class C, int MODE, int FMT>
 __global__ __launch_bounds__(256) void rmsnorm_generic(
     const void* __restrict__ x, const void* __restrict__ res, const void* __restrict__ w,
     void* __restrict__ y, uint8_t* __restrict__ yq, float* __restrict__ scale,
     void* __restrict__ ro, int64_t rows, int64_t cols, float eps, float static_scale) {
-  constexpr int VEC = C::VEC;
   __shared__ uint32_t lds[2 * 4];
-  __shared__ float group_sum[4];
-  int parity = 0;
+  __shared__ float stage[4 * kRegionAddends];
+  __shared__ float blocks[2 * 4 * kFoldLanes];
+  __shared__ float tail[2 * kTailWords];
+  int parity = 0, rpar = 0;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t nvec = (cols + VEC - 1) / VEC;
-  const int64_t ngroups = (nvec + 63) / 64;
+  const AtenSumPlan pl(cols);
+  const int64_t nsub = int64_t(1) << (pl.p - 4);  // regions per block
+  const int64_t bvecs = kRegionVecs * nsub;       // vectors per block
+  const int64_t nblk = pl.nfull + (pl.has_tail() ? 1 : 0);
+  float* a = stage + wave * kRegionAddends;
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const int64_t base = row * cols;
-    float total = 0.0f;
-    for (int64_t g0 = 0; g0 < ngroups; g0 += 4) {
-      const int64_t v = (g0 + wave) * 64 + lane;
-      float part = 0.0f;
-      if (v < nvec) {
+    AtenCascade cs;
+    int tpar = 0;
+    for (int64_t b0 = 0; b0 < nblk; b0 += 4) {
+      const int64_t blk = b0 + wave;
+      float* bs = blocks + rpar * 4 * kFoldLanes;
+      float* tl = tail + rpar * kTailWords;
+      if (blk < nblk) {
+        const bool full = blk < pl.nfull;
+        float fold = 0.0f;
+        for (int64_t sb = 0; sb < nsub; ++sb) {
+          const int64_t first = blk * bvecs + sb * kRegionVecs;
+          if (first * kSumLanes >= cols) break;
+          const int64_t v = first + lane;
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) {
-          const int64_t j = v * VEC + i;
-          if (j < cols) {
-            const float o = C::round(C::load1(x, base + j) + C::load1(res, base + j));
-            C::store1(ro, base + j, o);
-            part += o * o;
+          for (int i = 0; i < kSumLanes; ++i) {
+            const int64_t j = v * kSumLanes + i;
+            float sqv = 0.0f;
+            if (j < cols) {
+              const float o = C::round(C::load1(x, base + j) + C::load1(res, base + j));
+              C::store1(ro, base + j, o);
+              sqv = o * o;
+            }
+            a[lane * kSumLanes + i] = sqv;
+          }
+          __builtin_amdgcn_wave_barrier();
+          int nst = 16;
+          if (!full) {
+            const int64_t left = pl.ntrail - sb * 16;
+            nst = left < 0 ? 0 : (left > 16 ? 16 : (int)left);
+          }
+          fold = fold_region(a, nst, lane & 31, fold);
+          if (!full) stage_tail_parts(pl, a, first, lane, tl);
+          __builtin_amdgcn_wave_barrier();
+        }
+        if (lane < kFoldLanes) {
+          if (full) {
+            bs[wave * kFoldLanes + lane] = fold;
+          } else {
+            tl[lane] = fold;
           }
         }
       }
-      const float gs = bits_f32(wave_allreduce(f32_bits(part), AddF32{}));
-      if (lane == 0) group_sum[wave] = gs;
       __syncthreads();
-      for (int i = 0; i < 4 && g0 + i < ngroups; ++i) total += group_sum[i];
-      __syncthreads();
+      if (lane < kFoldLanes) {
+        for (int i = 0; i < 4; ++i) {
+          if (b0 + i < pl.nfull) cs.add_block(bs[i * kFoldLanes + lane], b0 + i, pl.p);
+        }
+      }
+      tpar = rpar;
+      rpar ^= 1;
     }
+    const float total = aten_finish(pl, cs, tail + tpar * kTailWords, lane);
     const float inv = 1.0f / __builtin_sqrtf(total / (float)cols + eps);
     if constexpr (MODE == 0) {
       for (int64_t j = threadIdx.x; j < cols; j += 256) {
@@ -314,15 +364,23 @@ int32_t launch_rmsnorm(const void* x, const void* res, const void* w, void* y, u
   // against 44.6 / 76.1 at two per thread), two per thread for the per-token
   // FP8 variant, whose extra amax reduction prefers fewer waves per row
   // (76.1 us against 77.7).
+  // fp32 rows stage their squares whole in LDS (aten_sum.hpp), so they stop
+  // at 1024 x 2 vectors (8192 elements, 32 KB); longer ones loop.
   bool done;
-  if constexpr (MODE != 1) {
+  if constexpr (MODE != 1 && C::VEC == 8) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<512, 1>,
                                     RowShape<1024, 1>, RowShape<1024, 2>,
                                     RowShape<1024, 4>>(nvec, run);
-  } else {
+  } else if constexpr (MODE != 1) {
+    done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<512, 1>,
+                                    RowShape<1024, 1>, RowShape<1024, 2>>(nvec, run);
+  } else if constexpr (C::VEC == 8) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
                                     RowShape<512, 2>, RowShape<1024, 2>,
                                     RowShape<1024, 4>>(nvec, run);
+  } else {
+    done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
+                                    RowShape<512, 2>, RowShape<1024, 2>>(nvec, run);
   }
   if (!done) {
     rmsnorm_generic<C, MODE, FMT><<<g, 256, 0, st>>>(x, res, w, y, yq, scale, ro, rows, cols, eps, static_scale);

@@ -40,15 +40,12 @@ def bits_equal(actual: torch.Tensor, expected: torch.Tensor) -> np.ndarray:
     return (ai == ei) | (np.isnan(a.float().numpy()) & np.isnan(e.float().numpy()))
 
 
-# Per storage type: (one ulp relative, hard cap, allowed fraction above one ulp;
-# 1e-5 is the reference's own outlier budget, tests/numerics.py:26).
-# An element above one ulp comes from eager's double rounding: when the fp32
-# intermediate sits within an fp32 ulp of a rounding midpoint of the storage
-# type, a one-ulp difference in that intermediate becomes up to two ulps in
-# the next product (e.g. T(normed) * weight).
+# Per storage type: (one ulp relative, hard cap, allowed fraction above one
+# ulp). The north-star bound is one ulp for every element (bf16 2^-7, fp16
+# 2^-10, fp32 1e-5 relative), so nothing may exceed it.
 ULP_TOL = {
-    torch.bfloat16: (2.0 ** -7, 2.0 ** -6, 1e-5),
-    torch.float16: (2.0 ** -10, 2.0 ** -9, 1e-5),
+    torch.bfloat16: (2.0 ** -7, 2.0 ** -7, 0.0),
+    torch.float16: (2.0 ** -10, 2.0 ** -10, 0.0),
     torch.float32: (1e-5, 1e-5, 0.0),
 }
 

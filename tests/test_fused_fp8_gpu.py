@@ -1,13 +1,19 @@
-"""Fused RMSNorm+FP8 and SwiGLU+FP8 kernels.
+"""Fused RMSNorm+FP8 and SwiGLU+FP8 kernels against the composed eager oracle
+(the eager op of baselines/rmsnorm_residual.py:123-136 or baselines/swiglu.py:107-112,
+then the per-row or static quantisation of baselines/fp8_quant.py:162-178
+applied to its output as stored in its dtype).
 
-Parity definition (a fused op's codes depend on its own bf16 intermediate):
-* codes and scales are bit-exact against the oracle quantisation of the
-  kernel's own intermediate, produced by the unfused kernel of this library
-  (which is itself checked against the eager oracle within one ulp in
-  test_rmsnorm_residual_gpu.py / test_swiglu_gpu.py);
-* residual_out is bit-exact against the eager oracle;
-* the fraction of codes that also equal the strict composed-eager oracle is
-  printed (it differs only where the intermediate is one ulp apart).
+* RMSNorm+FP8, every dtype: codes and scales bit-exact against the composed
+  eager oracle (the kernel's y equals the eager y bit for bit), and
+  residual_out bit-exact;
+* SwiGLU+FP8, bf16 / fp16: codes and scales bit-exact against the composed
+  eager oracle;
+* SwiGLU+FP8, fp32: codes and scales bit-exact against the oracle's
+  quantisation of the library's own unfused SwiGLU output; every code that
+  differs from the composed eager oracle must sit where that output differs
+  from torch's (torch-CPU's fp32 sigmoid is not correctly rounded; the
+  output itself is held to 1e-5 relative in test_swiglu_gpu.py). Mismatch
+  counts are printed.
 Workloads: BASELINE configs 3v and 5 (per-token and static 0.05) at full size,
 plus small and ragged shapes in all dtypes / formats.
 """
@@ -35,30 +41,47 @@ def _quant(y: torch.Tensor, fmt, static):
     return ofp8.quant_static(y2, static, fmt), np.array([static], dtype=np.float32)
 
 
+def _scales_ref(s_ref, static):
+    return s_ref if static is None else np.array([static], dtype=np.float32)
+
+
 def _check_rms(x, r, w, eps, fmt, static):
     xd, rd, wd = x.cuda(), r.cuda(), w.cuda()
     q, s, ro = rmsnorm_residual_fp8(xd, rd, wd, eps, fp8_format=fmt, scale=static)
-    y_k, _ = rmsnorm_residual(xd, rd, wd, eps)
-    codes, s_ref = _quant(y_k, fmt, static)
-    assert_codes_equal(q, codes.reshape(q.shape))
-    assert_f32_bits_equal(s, s_ref.reshape(s.shape) if static is None else s_ref)
-    _, ro_ref = eager.rmsnorm_residual(x, r, w, eps)
-    assert bits_equal(ro, ro_ref).all()
-    strict, _, _, _ = eager.rmsnorm_residual_fp8(x, r, w, eps, fmt, static)
+    strict, s_ref, ro_ref, _ = eager.rmsnorm_residual_fp8(x, r, w, eps, fmt, static)
+    n_bad = int((codes_np(q).reshape(strict.shape) != strict).sum())
     print(f"\nrmsnorm+fp8 {tuple(x.shape)} {x.dtype} {fmt} static={static}: "
-          f"strict-eager code agreement {float((codes_np(q).reshape(strict.shape) == strict).mean()):.7f}")
+          f"{n_bad} of {strict.size} codes differ from the composed eager oracle")
+    assert_codes_equal(q, strict.reshape(q.shape))
+    s_ref = _scales_ref(s_ref, static)
+    assert_f32_bits_equal(s, s_ref.reshape(s.shape) if static is None else s_ref)
+    assert bits_equal(ro, ro_ref).all()
 
 
 def _check_swiglu(g, u, fmt, static):
     gd, ud = g.cuda(), u.cuda()
     q, s = swiglu_fp8(gd, ud, fp8_format=fmt, scale=static)
+    strict, s_strict, y_ref = eager.swiglu_fp8(g, u, fmt, static)
+    qn = codes_np(q).reshape(strict.shape)
+    n_bad = int((qn != strict).sum())
+    print(f"\nswiglu+fp8 {tuple(g.shape)} {g.dtype} {fmt} static={static}: "
+          f"{n_bad} of {strict.size} codes differ from the composed eager oracle")
+    if g.dtype != torch.float32:
+        assert_codes_equal(q, strict.reshape(q.shape))
+        s_strict = _scales_ref(s_strict, static)
+        assert_f32_bits_equal(s, s_strict.reshape(s.shape) if static is None else s_strict)
+        return
     y_k = swiglu(gd, ud)
     codes, s_ref = _quant(y_k, fmt, static)
     assert_codes_equal(q, codes.reshape(q.shape))
     assert_f32_bits_equal(s, s_ref.reshape(s.shape) if static is None else s_ref)
-    strict, _, _ = eager.swiglu_fp8(g, u, fmt, static)
-    print(f"\nswiglu+fp8 {tuple(g.shape)} {g.dtype} {fmt} static={static}: "
-          f"strict-eager code agreement {float((codes_np(q).reshape(strict.shape) == strict).mean()):.7f}")
+    y_diff = ~bits_equal(y_k, y_ref).reshape(strict.shape)
+    code_diff = qn != strict
+    if static is None:
+        # a row whose scale moved can change any code of the row
+        row_moved = ~bits_equal(s.cpu(), torch.from_numpy(s_strict)).reshape(-1)
+        code_diff[row_moved.reshape(-1)] = False
+    assert not (code_diff & ~y_diff).any(), "a code differs where the fp32 SwiGLU output equals torch's"
 
 
 @pytest.mark.parametrize("static", [None, 0.05])

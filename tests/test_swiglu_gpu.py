@@ -1,7 +1,8 @@
 """SwiGLU kernel vs the CPU oracle (torch-CPU restatement of
-baselines/swiglu.py:107-112): within one storage-type ulp relative (bf16
-2^-7, fp16 2^-10), 1e-5 relative in fp32 (rare two-ulp elements bounded as in
-tests/_parity.py ULP_TOL). Shapes: the reference's case table
+baselines/swiglu.py:107-112): bit-exact in bf16 and fp16, and every element
+within one storage-type ulp relative (bf16 2^-7, fp16 2^-10) or 1e-5
+relative in fp32 (torch-CPU's fp32 sigmoid is not correctly rounded, so fp32
+agrees to the bound, not bit for bit). Shapes: the reference's case table
 (baselines/swiglu.py:70-88), the vector-tail sizes n = 1..129 its kernel
 tests sweep (tests/test_swiglu_kernel.py:74-93), BASELINE config 3 at full size,
 and every one of the 65536 bf16 gate values, alone and shuffled among
@@ -33,6 +34,8 @@ def _run(g, u):
         return None
     stats = assert_ulp_close(y, y_ref, "y")
     print(f"\n{tuple(g.shape)} {g.dtype}: {stats}")
+    if g.dtype != torch.float32:
+        assert stats["bit_exact_fraction"] == 1.0, stats
     return stats
 
 
@@ -55,7 +58,7 @@ def test_config3_full_size():
     rows, cols = inputs.CONFIG_SHAPES["swiglu"]
     g, u = inputs.swiglu_inputs(rows, cols, torch.bfloat16, seed=0)
     stats = _run(g, u)
-    assert stats["bit_exact_fraction"] > 0.999
+    assert stats["violations"] == 0 and stats["bit_exact_fraction"] == 1.0
 
 
 def test_extreme_gate_values():
