@@ -61,11 +61,6 @@ __device__ inline float readlane_f32(float v, int lane) {
   return bits_f32((uint32_t)__builtin_amdgcn_readlane((int)f32_bits(v), lane));
 }
 
-// Bitmask-mode ds_swizzle within 32-lane halves: lane i reads lane i ^ X.
-template <int X>
-__device__ inline float swizzle_xor(float v) {
-  return bits_f32((uint32_t)__builtin_amdgcn_ds_swizzle((int)f32_bits(v), (X << 10) | 0x1f));
-}
 
 // Continue the folds of lanes c < 32 over `nsteps` steps of a staged region.
 __device__ inline float fold_region(const float* a, int nsteps, int c, float acc) {
@@ -79,58 +74,107 @@ __device__ inline float fold_region16(const float* a, int c) {
   return acc;
 }
 
-// The cascade state of the 32 folds (lanes c < 32; every wave keeps a copy).
-struct AtenCascade {
+// Tail data of a row, staged by the wave that holds the last region:
+//   [0, 32)  the folds of the trailing steps (acc0), fold c at word c;
+//   [32, 56) the squares of the leftover vectors, 8 per vector;
+//   [56, 64) the trailing scalars.
+constexpr int kTailWords = 64;
+
+// The addends here are squares, never -0, so every partial sum is +0, a
+// positive number, +inf or NaN, and adding a +0 leaves it unchanged. Where
+// the order adds a level that is still zero (or a zero acc0), the addition
+// is skipped without changing a bit.
+
+// The cascade of fold c (slot c / 8, lane c % 8) of one row, in lane c < 32.
+struct FoldCascade {
   float a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-  // Add the fold of whole block `b` (0-based) of a row with block exponent p.
-  __device__ void add_block(float f, int64_t b, int p) {
+  bool has2 = false, has3 = false;
+  // Add the fold f of whole block b of a row with block exponent p.
+  __device__ void add(float f, int64_t b, int p) {
     a1 = a1 + f;
     const int64_t done = b + 1;
     if ((done & ((int64_t(1) << p) - 1)) == 0) {
       a2 = a2 + a1;
       a1 = 0.0f;
+      has2 = true;
       if ((done & ((int64_t(1) << (2 * p)) - 1)) == 0) {
         a3 = a3 + a2;
         a2 = 0.0f;
+        has3 = true;
       }
     }
   }
+  // ((acc0 + acc1) + acc2) + acc3 with acc0 the trailing steps' fold.
+  __device__ float slot_sum(const AtenSumPlan& pl, const float* tail, int c) const {
+    float q = a1;
+    if (pl.ntrail) q = tail[c] + q;
+    if (has2) q = q + a2;
+    if (has3) q = q + a3;
+    return q;
+  }
 };
 
-// Tail data of a row, staged by the wave that holds the last region:
-//   [0, 32)  the folds of the trailing steps (acc0);
-//   [32, 56) the squares of the leftover vectors, 8 per vector;
-//   [56, 64) the trailing scalars.
-constexpr int kTailWords = 64;
+// Bitmask-mode ds_swizzle within 32-lane halves: lane i reads lane i ^ X.
+template <int X>
+__device__ inline float swizzle_xor(float v) {
+  return bits_f32((uint32_t)__builtin_amdgcn_ds_swizzle((int)f32_bits(v), (X << 10) | 0x1f));
+}
 
-// Finish the row sum from the cascade state and the staged tail (every lane
-// of the wave must be active; the result is wave-uniform).
-__device__ inline float aten_finish(const AtenSumPlan& pl, const AtenCascade& cs, const float* tail, int lane) {
-  if (pl.nv == 0) {
-    // Scalar rows (n < 8): slots of single elements.
-    const int n = pl.ntail;
-    const int s = n / 4;
-    float p0 = s ? 0.0f + tail[56] : 0.0f;
-    for (int e = 4 * s; e < n; ++e) p0 = p0 + tail[56 + e];
-    for (int k = 1; k < 4; ++k) p0 = p0 + (s ? 0.0f + tail[56 + k] : 0.0f);
-    return 0.0f + p0;
+// From the slot sums q of lanes c < 32 (0 elsewhere) to the row total: the
+// leftover vectors into slot 0, the slots combined in order in lanes 0..7,
+// then ((0 + trailing scalars) + lane 0) + ... + lane 7. Every lane of the
+// wave must be active; the result is wave-uniform.
+__device__ inline float aten_combine(const AtenSumPlan& pl, float q, const float* tail, int lane) {
+  if (lane < kSumLanes) {
+    for (int i = 0; i < pl.nleft; ++i) q = q + tail[32 + kSumLanes * i + lane];
   }
-  float v = 0.0f;
-  if (lane < kFoldLanes) {
-    const float a0 = pl.ntrail ? tail[lane] : 0.0f;
-    v = ((a0 + cs.a1) + cs.a2) + cs.a3;
-    if (lane < kSumLanes) {
-      for (int i = 0; i < pl.nleft; ++i) v = v + tail[32 + kSumLanes * i + lane];
-    }
-  }
-  // Lanes 0..7: ((slot 0 + slot 1) + slot 2) + slot 3.
-  const float v1 = swizzle_xor<8>(v), v2 = swizzle_xor<16>(v), v3 = swizzle_xor<24>(v);
-  const float p = ((v + v1) + v2) + v3;
+  const float q1 = swizzle_xor<8>(q), q2 = swizzle_xor<16>(q), q3 = swizzle_xor<24>(q);
+  const float p = ((q + q1) + q2) + q3;
   float t = 0.0f;
   for (int e = 0; e < pl.ntail; ++e) t = t + tail[56 + e];
+  t = t + readlane_f32(p, 0);
 #pragma unroll
-  for (int l = 0; l < kSumLanes; ++l) t = t + readlane_f32(p, l);
+  for (int l = 1; l < kSumLanes; ++l) t = t + readlane_f32(p, l);
   return t;
+}
+
+// Rows under 8 addends: four slots of single elements, leftovers into slot
+// 0, slots combined in order (the scalars are tail words 56..).
+__device__ inline float aten_scalar_row(const AtenSumPlan& pl, const float* tail) {
+  const int n = pl.ntail;
+  const int s = n / 4;
+  float p0 = s ? tail[56] : 0.0f;
+  for (int e = 4 * s; e < n; ++e) p0 = p0 + tail[56 + e];
+  for (int k = 1; k < 4; ++k) p0 = p0 + (s ? tail[56 + k] : 0.0f);
+  return p0;
+}
+
+// Finish the row sum from all its block folds `bs` (nfull blocks of 32
+// words) and the staged tail, for rows with 16-step blocks (P = 4). MAXB
+// bounds nfull at compile time. Up to 16 blocks the level-2 promotion can
+// only happen after the 16th and last block, where it moves acc1 to acc2
+// unchanged, so the cascade is one running sum; its loads are all issued
+// before the first addition (blocks past the row are read and not used).
+template <int MAXB>
+__device__ inline float aten_finish(const AtenSumPlan& pl, const float* bs, const float* tail, int lane) {
+  if (pl.nv == 0) return aten_scalar_row(pl, tail);
+  float q = 0.0f;
+  if (lane < kFoldLanes) {
+    if constexpr (MAXB <= 16) {
+      float f[MAXB];
+#pragma unroll
+      for (int b = 0; b < MAXB; ++b) f[b] = bs[b * kFoldLanes + lane];
+      q = pl.nfull ? f[0] : 0.0f;
+#pragma unroll
+      for (int b = 1; b < MAXB; ++b) q = (b < pl.nfull) ? q + f[b] : q;
+      if (pl.ntrail) q = tail[lane] + q;
+    } else {
+      FoldCascade cs;
+      for (int b = 0; b < pl.nfull; ++b) cs.add(bs[b * kFoldLanes + lane], b, 4);
+      q = cs.slot_sum(pl, tail, lane);
+    }
+  }
+  return aten_combine(pl, q, tail, lane);
 }
 
 // Copy the leftover vectors and trailing scalars that fall in a staged region
@@ -154,8 +198,11 @@ __device__ inline void stage_tail_parts(const AtenSumPlan& pl, const float* a, i
 // most 2^23 addends). The kernel hands each vector's squares to item(k, sq)
 // as soon as it has them (zeros past the row), then calls total().
 //   VEC == 8: one 16-byte vector is one 8-lane vector, so item k of wave w
-//     is region w + NW * k whole; the wave stages it in its own 512 floats of
-//     `stage` and folds it at once, without waiting for the other waves;
+//     is region w + NW * k whole. The wave stages its regions in its own part
+//     of `stage` and folds them without waiting for the other waves; a fold
+//     needs 32 lanes, so the two halves of the wave fold two regions at once
+//     (SLOTS = 2 staged regions per wave) where the shape has two or more
+//     items per thread;
 //   VEC == 4: two waves share a region, so the row is staged whole in `stage`
 //     (THREADS * ITEMS * 4 floats) and folded behind a barrier.
 // `bsum` holds 2 x NREG x 32 floats and `tail` 2 x 64, alternated by `parity`
@@ -165,7 +212,8 @@ template <int VEC, int THREADS, int ITEMS>
 struct ResidentRowSum {
   static constexpr int NW = THREADS / 64;
   static constexpr int NREG = (THREADS * ITEMS * VEC + kRegionAddends - 1) / kRegionAddends;
-  static constexpr int kStageFloats = VEC == 8 ? NW * kRegionAddends : THREADS * ITEMS * VEC;
+  static constexpr int SLOTS = (ITEMS >= 2 && NW <= 8) ? 2 : 1;
+  static constexpr int kStageFloats = VEC == 8 ? NW * SLOTS * kRegionAddends : THREADS * ITEMS * VEC;
   const AtenSumPlan& pl;
   float* stage;
   float* bs;
@@ -177,28 +225,32 @@ struct ResidentRowSum {
     w = threadIdx.x >> 6;
     nreg = (int)pl.nfull + (pl.has_tail() ? 1 : 0);
   }
-  __device__ void fold_one(const float* a, int reg) {
+  // Fold region `reg` staged at `a`, as fold c (c < 32) of this lane.
+  __device__ void fold_one(const float* a, int reg, int c) {
     if (reg < pl.nfull) {
-      const float f = fold_region16(a, lane & 31);
-      if (lane < kFoldLanes) bs[reg * kFoldLanes + lane] = f;
+      bs[reg * kFoldLanes + c] = fold_region16(a, c);
     } else {
-      const float f = fold_region(a, pl.ntrail, lane & 31, 0.0f);
-      if (lane < kFoldLanes) tl[lane] = f;
-      stage_tail_parts(pl, a, (int64_t)reg * kRegionVecs, lane, tl);
+      tl[c] = fold_region(a, pl.ntrail, c, 0.0f);
+      stage_tail_parts(pl, a, (int64_t)reg * kRegionVecs, c, tl);
     }
   }
   __device__ void item(int k, const float (&sq)[VEC]) {
     if constexpr (VEC == 8) {
-      const int reg = w + NW * k;
-      if (reg < nreg) {
-        float* a = stage + w * kRegionAddends;
+      if (w + NW * k < nreg) {
+        float* a = stage + (w * SLOTS + k % SLOTS) * kRegionAddends;
 #pragma unroll
         for (int i = 0; i < VEC; ++i) a[lane * VEC + i] = sq[i];
+      }
+      if (k % SLOTS == SLOTS - 1 || k == ITEMS - 1) {
         // LDS accesses of one wave complete in order; the wave barriers only
-        // keep the compiler from moving the fold's reads above these writes,
-        // or the next item's writes above the fold's reads.
+        // keep the compiler from moving the fold's reads above the staging
+        // writes, or the next staging writes above the fold's reads.
         __builtin_amdgcn_wave_barrier();
-        fold_one(a, reg);
+        const int h = lane >> 5;
+        const int kk = k - k % SLOTS + h;  // the item this half folds
+        if (kk < ITEMS && (SLOTS == 2 || h == 0) && w + NW * kk < nreg) {
+          fold_one(stage + (w * SLOTS + h) * kRegionAddends, w + NW * kk, lane & 31);
+        }
         __builtin_amdgcn_wave_barrier();
       }
     } else {
@@ -211,14 +263,12 @@ struct ResidentRowSum {
   __device__ float total() {
     if constexpr (VEC != 8) {
       __syncthreads();
-      for (int reg = w; reg < nreg; reg += NW) fold_one(stage + reg * kRegionAddends, reg);
+      for (int reg = 2 * w + (lane >> 5); reg < nreg; reg += 2 * NW) {
+        fold_one(stage + reg * kRegionAddends, reg, lane & 31);
+      }
     }
     __syncthreads();
-    AtenCascade cs;
-    if (lane < kFoldLanes) {
-      for (int b = 0; b < pl.nfull; ++b) cs.add_block(bs[b * kFoldLanes + lane], b, 4);
-    }
-    return aten_finish(pl, cs, tl, lane);
+    return aten_finish<NREG>(pl, bs, tl, lane);
   }
 };
 

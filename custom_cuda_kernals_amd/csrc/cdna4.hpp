@@ -26,6 +26,7 @@ enum : int32_t { kF32 = 0, kF16 = 1, kBF16 = 2, kF8E4M3 = 3, kF8E5M2 = 4 };
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
 using f32x2 = float __attribute__((ext_vector_type(2)));
+using f32x4 = float __attribute__((ext_vector_type(4)));
 using bf16x2 = __bf16 __attribute__((ext_vector_type(2)));
 using f16x2 = _Float16 __attribute__((ext_vector_type(2)));
 using u16x2 = uint16_t __attribute__((ext_vector_type(2)));

@@ -94,16 +94,10 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
       if (v < nvec) wreg[k] = wv[v];
     }
   }
-  // The FP8 modes issue a row's loads one iteration ahead: the first row's
-  // right here, each next row's before the current row is reduced (74.7 vs
-  // 75.7 us per-token and 74.1 vs 74.7 us static at [16384, 4096] bf16 on
-  // MI355X, although the second set of row registers costs occupancy). The
-  // plain op loads in the loop (43.4 us against 43.9 ahead).
-  constexpr bool kAhead = MODE != 0;
-  u32x4 nx[kAhead ? ITEMS : 1], nr[kAhead ? ITEMS : 1];
-  if constexpr (kAhead) {
-    if ((int64_t)blockIdx.x < rows) load_row(blockIdx.x, nx, nr);
-  }
+  // A workgroup's first row is loaded at kernel entry, ahead of the loop
+  // set-up; later rows (beyond the workgroup cap) load in the loop.
+  u32x4 xa[ITEMS], ra[ITEMS];
+  if ((int64_t)blockIdx.x < rows) load_row(blockIdx.x, xa, ra);
   int parity = 0;
   // Rows go to workgroups in blockIdx order, which the dispatcher deals to the
   // 8 XCDs round-robin; measured on MI355X, this beats giving each XCD a
@@ -111,17 +105,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x, parity ^= 1) {
     const int64_t off = row * cols * C::kBytes;
     const RowBuf<true, ro_store_policy(MODE)> bro(static_cast<char*>(ro) + off, row_bytes);
-    u32x4 xa[ITEMS], ra[ITEMS];
-    if constexpr (kAhead) {
-#pragma unroll
-      for (int k = 0; k < ITEMS; ++k) {
-        xa[k] = nx[k];
-        ra[k] = nr[k];
-      }
-      if (row + gridDim.x < rows) load_row(row + gridDim.x, nx, nr);
-    } else {
-      load_row(row, xa, ra);
-    }
+    if (row != (int64_t)blockIdx.x) load_row(row, xa, ra);
     u32x4 rov[ITEMS];
     // torch-CPU's summation order, which does not depend on the launch
     // shape either: the plain and the FP8 variants (different shapes) give
@@ -261,7 +245,7 @@ __global__ __launch_bounds__(256) void rmsnorm_generic(
   float* a = stage + wave * kRegionAddends;
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const int64_t base = row * cols;
-    AtenCascade cs;
+    FoldCascade cs;
     int tpar = 0;
     for (int64_t b0 = 0; b0 < nblk; b0 += 4) {
       const int64_t blk = b0 + wave;
@@ -306,13 +290,15 @@ __global__ __launch_bounds__(256) void rmsnorm_generic(
       __syncthreads();
       if (lane < kFoldLanes) {
         for (int i = 0; i < 4; ++i) {
-          if (b0 + i < pl.nfull) cs.add_block(bs[i * kFoldLanes + lane], b0 + i, pl.p);
+          if (b0 + i < pl.nfull) cs.add(bs[i * kFoldLanes + lane], b0 + i, pl.p);
         }
       }
       tpar = rpar;
       rpar ^= 1;
     }
-    const float total = aten_finish(pl, cs, tail + tpar * kTailWords, lane);
+    const float* tl = tail + tpar * kTailWords;
+    const float total = pl.nv == 0 ? aten_scalar_row(pl, tl)
+                                   : aten_combine(pl, lane < kFoldLanes ? cs.slot_sum(pl, tl, lane) : 0.0f, tl, lane);
     const float inv = 1.0f / __builtin_sqrtf(total / (float)cols + eps);
     if constexpr (MODE == 0) {
       for (int64_t j = threadIdx.x; j < cols; j += 256) {
@@ -360,18 +346,18 @@ int32_t launch_rmsnorm(const void* x, const void* res, const void* w, void* y, u
         x, res, w, y, yq, scale, ro, rows, cols, eps, static_scale);
   };
   // Shapes measured on MI355X at cols = 4096 bf16: one vector per thread is
-  // fastest for the plain op and the static-scale FP8 variant (44.1 / 75.5 us,
-  // against 44.6 / 76.1 at two per thread), two per thread for the per-token
-  // FP8 variant, whose extra amax reduction prefers fewer waves per row
-  // (76.1 us against 77.7).
+  // fastest for the plain op (45.0 us against 45.3-46.0 at two per thread);
+  // two per thread for the FP8 variants, whose extra registers (the y values
+  // held across the amax reduction) and extra reduction prefer fewer waves
+  // per row (static scale: 76.2 us against 98.1 at one per thread).
   // fp32 rows stage their squares whole in LDS (aten_sum.hpp), so they stop
   // at 1024 x 2 vectors (8192 elements, 32 KB); longer ones loop.
   bool done;
-  if constexpr (MODE != 1 && C::VEC == 8) {
+  if constexpr (MODE == 0 && C::VEC == 8) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<512, 1>,
                                     RowShape<1024, 1>, RowShape<1024, 2>,
                                     RowShape<1024, 4>>(nvec, run);
-  } else if constexpr (MODE != 1) {
+  } else if constexpr (MODE == 0) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<512, 1>,
                                     RowShape<1024, 1>, RowShape<1024, 2>>(nvec, run);
   } else if constexpr (C::VEC == 8) {
