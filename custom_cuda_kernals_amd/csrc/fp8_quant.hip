@@ -289,6 +289,7 @@ __global__ __launch_bounds__(256) void fp8_block_generic(const void* __restrict_
 // ---------------------------------------------------------------------------
 constexpr int kPartialThreads = 512, kPartialUnroll = 4, kPartialMaxGroups = 512;
 
+// Each workgroup stores its max |x| bits into partial[blockIdx.x].
 template <class C, bool VECTOR>
 __global__ __launch_bounds__(kPartialThreads) void fp8_tensor_partial(const void* __restrict__ x, int64_t total,
                                                                       uint32_t* __restrict__ partial) {
@@ -356,12 +357,43 @@ __global__ __launch_bounds__(256) void fp8_tensor_amax(const void* __restrict__ 
 // against 256 threads with one vector per grid-stride step and cached code
 // stores: 32.3 vs 35.7 us at [16384, 4096] bf16, 248 vs 338 us at [65536, 8192].
 constexpr int kCastThreads = 512, kCastUnroll = 2;
+static_assert(kPartialThreads * kPartialUnroll == 2 * kCastThreads * kCastUnroll,
+              "the XCD-aligned cast order takes halves of the partial pass's chunks");
 
 template <class C, int FMT, bool STATIC, bool VECTOR>
 __global__ __launch_bounds__(VECTOR ? kCastThreads : 256) void fp8_tensor_cast(
     const void* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ scale_out,
-    const int32_t* __restrict__ amax_bits, float static_scale, int64_t total) {
+    const int32_t* __restrict__ amax_bits, float static_scale, int64_t total, bool xcd_aligned = false) {
   constexpr int T = VECTOR ? kCastThreads : 256;
+  constexpr int U = VECTOR ? kCastUnroll : 1;
+  const int64_t nvec = VECTOR ? total / C::VEC : 0;
+  const u32x4* xv = static_cast<const u32x4*>(x);
+  int64_t bid = blockIdx.x;
+  if constexpr (!STATIC) {
+    // After the partial pass. When both passes cover x in one round of
+    // workgroups (the partial's grid a multiple of 8, this one a multiple
+    // of 16), workgroup 8a + c re-reads a half of partial chunk
+    // 8 (a / 2) + c: workgroups are dealt to the 8 XCDs round-robin, so
+    // that half was read by the same XCD and is still in its L2 (12.4-12.7
+    // vs 13.4-13.6 us for the whole reference-ABI op at [2048, 4096] bf16 on
+    // MI355X). Otherwise the chunks are walked last-first, starting on the
+    // most recently read part of x.
+    if (xcd_aligned) {
+      const int64_t a = blockIdx.x / 8, c = blockIdx.x % 8;
+      bid = 2 * (8 * (a / 2) + c) + (a % 2);
+    } else {
+      bid = gridDim.x - 1 - blockIdx.x;
+    }
+  }
+  int64_t b = bid * T * U + threadIdx.x;
+  u32x4 raw[U];
+  auto load = [&](int64_t b0) {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      if (b0 + k * T < nvec) raw[k] = ld_stream(xv + b0 + k * T);
+    }
+  };
+  if constexpr (VECTOR) load(b);
   float s, amax_t = 0.0f;
   if constexpr (STATIC) {
     s = static_scale;
@@ -374,20 +406,9 @@ __global__ __launch_bounds__(VECTOR ? kCastThreads : 256) void fp8_tensor_cast(
   const bool fast_t = fast_path_ok<FMT>(s, r, amax_t);
   int64_t done = 0;
   if constexpr (VECTOR) {
-    constexpr int U = kCastUnroll;
-    const int64_t nvec = total / C::VEC;
-    const u32x4* xv = static_cast<const u32x4*>(x);
-    // After the partial pass the dynamic-scale cast walks the workgroups'
-    // chunks last-first, so it starts on the most recently read part of x:
-    // 13.3 vs 13.6 us for the whole op at [2048, 4096] bf16 (no change at
-    // [16384, 4096]).
-    const int64_t bid = STATIC ? (int64_t)blockIdx.x : (int64_t)(gridDim.x - 1 - blockIdx.x);
-    for (int64_t b = bid * T * U + threadIdx.x; b < nvec; b += (int64_t)gridDim.x * T * U) {
-      u32x4 raw[U];
-#pragma unroll
-      for (int k = 0; k < U; ++k) {
-        if (b + k * T < nvec) raw[k] = ld_stream(xv + b + k * T);
-      }
+    const int64_t stride = (int64_t)gridDim.x * T * U;
+    for (; b < nvec; b += stride) {
+      if (b != bid * T * U + threadIdx.x) load(b);
 #pragma unroll
       for (int k = 0; k < U; ++k) {
         const int64_t v = b + k * T;
@@ -407,6 +428,16 @@ __global__ __launch_bounds__(VECTOR ? kCastThreads : 256) void fp8_tensor_cast(
     if constexpr (STATIC) fast = fast_path_ok<FMT>(s, r, __builtin_fabsf(v));
     q[i] = quant1<FMT>(v, s, r, fast);
   }
+}
+
+// Cast grid for a dynamic-scale tensor after the partial pass over `gp`
+// workgroups, and whether the XCD-aligned chunk order applies (both passes
+// one round of workgroups, grids multiples of 8 and 16).
+inline unsigned tensor_cast_grid(int64_t nvec, unsigned gp, bool* xcd_aligned) {
+  const unsigned g = flat_grid(nvec, kCastThreads * kCastUnroll, 1 << 20);
+  *xcd_aligned = nvec <= (int64_t)kPartialMaxGroups * kPartialThreads * kPartialUnroll && g == 2 * gp &&
+                 gp % 8 == 0;
+  return g;
 }
 
 // Row-length buckets of the register-resident token kernel.
@@ -512,8 +543,10 @@ extern "C" int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, fl
         fp8_tensor_amax<C, false><<<1, 256, 0, st>>>(x, total, amax_scratch);
       }
       if (vec_ok) {
-        const unsigned g = flat_grid(total / C::VEC, kCastThreads * kCastUnroll, 1 << 20);
-        fp8_tensor_cast<C, FMT, false, true><<<g, kCastThreads, 0, st>>>(x, x_fp8, scale, amax_scratch, 0.0f, total);
+        bool aligned = false;
+        const unsigned g = tensor_cast_grid(total / C::VEC, slots_fit ? gp : 0u, &aligned);
+        fp8_tensor_cast<C, FMT, false, true><<<g, kCastThreads, 0, st>>>(x, x_fp8, scale, amax_scratch, 0.0f,
+                                                                          total, aligned);
       } else {
         const unsigned g = flat_grid(total / C::VEC, 256, 2048);
         fp8_tensor_cast<C, FMT, false, false><<<g, 256, 0, st>>>(x, x_fp8, scale, amax_scratch, 0.0f, total);
