@@ -17,6 +17,8 @@
 // whose scale is non-finite, or whose quotients leave the verified range of
 // the hardware conversion, take the exact path (x86-compatible division +
 // software encoder) as a workgroup-uniform branch.
+#include <mutex>
+
 #include "launch.hpp"
 
 namespace cck {
@@ -360,10 +362,14 @@ constexpr int kCastThreads = 512, kCastUnroll = 2;
 static_assert(kPartialThreads * kPartialUnroll == 2 * kCastThreads * kCastUnroll,
               "the XCD-aligned cast order takes halves of the partial pass's chunks");
 
-template <class C, int FMT, bool STATIC, bool VECTOR>
+// SLOTS: the dynamic scale comes from the `nslots` partial maxima in `slots`
+// (each workgroup reduces them itself; the first vectors' loads are issued
+// before that reduction), not from *amax_bits.
+template <class C, int FMT, bool STATIC, bool VECTOR, bool SLOTS = false>
 __global__ __launch_bounds__(VECTOR ? kCastThreads : 256) void fp8_tensor_cast(
     const void* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ scale_out,
-    const int32_t* __restrict__ amax_bits, float static_scale, int64_t total, bool xcd_aligned = false) {
+    const int32_t* __restrict__ amax_bits, float static_scale, int64_t total, bool xcd_aligned = false,
+    const uint32_t* __restrict__ slots = nullptr, int nslots = 0) {
   constexpr int T = VECTOR ? kCastThreads : 256;
   constexpr int U = VECTOR ? kCastUnroll : 1;
   const int64_t nvec = VECTOR ? total / C::VEC : 0;
@@ -398,7 +404,14 @@ __global__ __launch_bounds__(VECTOR ? kCastThreads : 256) void fp8_tensor_cast(
   if constexpr (STATIC) {
     s = static_scale;
   } else {
-    amax_t = bits_f32((uint32_t)*amax_bits);
+    if constexpr (SLOTS) {
+      __shared__ uint32_t lds[2 * (T / 64)];
+      uint32_t m = 0;
+      for (int i = threadIdx.x; i < nslots; i += T) m = max(m, slots[i]);
+      amax_t = bits_f32(block_allreduce<T / 64>(m, MaxU32{}, lds, 0));
+    } else {
+      amax_t = bits_f32((uint32_t)*amax_bits);
+    }
     s = scale_from_amax<FMT>(amax_t);
     if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
   }
@@ -456,6 +469,42 @@ int32_t launch_token(const void* x, uint8_t* q, float* scale, int64_t m, int64_t
                                              RowShape<1024, 8>>(nvec, run);
   if (!done) fp8_token_generic<C, FMT><<<g, 256, 0, st>>>(x, q, scale, m, n);
   return launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// Tensor granularity with no memory from the caller beyond the input and the
+// outputs (no counterpart in the reference; for callers that cannot allocate:
+// code under HIP graph capture, serving loops). The partial maxima live in
+// `scratch`, a file-scope device array of kPartialMaxGroups words (2 KiB):
+// the partial pass runs at most kPartialMaxGroups workgroups for any input
+// size, so every size fits, and every cast workgroup reduces the slots
+// itself, so no finishing kernel runs and nothing needs clearing (each call
+// writes every slot it reads). Every call on a device shares that device's
+// array: calls that overlap on one GPU (on different streams) race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint32_t scratch[kPartialMaxGroups];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+uint32_t* scratch_dev[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device. The
+// host-side name of the array is only a handle for the runtime: kernels are
+// given this address.
+int32_t scratch_address(uint32_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int32_t)e;
+  if (dev < 0 || dev >= kMaxDevices) return (int32_t)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int32_t)e;
+    scratch_dev[dev] = static_cast<uint32_t*>(p);
+  }
+  *out = scratch_dev[dev];
+  return (int32_t)hipSuccess;
 }
 
 }  // namespace
@@ -573,6 +622,40 @@ extern "C" int32_t launch_fp8_quant_static_fwd(const void* x, uint8_t* x_fp8, fl
       } else {
         const unsigned g = flat_grid(total / C::VEC, 256, 8192);
         fp8_tensor_cast<C, FMT, true, false><<<g, 256, 0, st>>>(x, x_fp8, nullptr, nullptr, scale, total);
+      }
+      return launch_status();
+    });
+  });
+}
+
+extern "C" int32_t launch_fp8_quant_tensor_noalloc_fwd(const void* x, uint8_t* x_fp8, float* scale, int64_t m,
+                                                       int64_t n, int32_t dtype, int32_t fp8_format,
+                                                       void* stream) {
+  if (m <= 0 || n <= 0) return (int32_t)hipSuccess;
+  if (m > INT64_MAX / n) return (int32_t)hipErrorInvalidValue;  // m * n does not fit int64
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t total = m * n;
+  return with_codec(dtype, [&](auto codec) {
+    using C = decltype(codec);
+    return with_fp8(fp8_format, [&](auto f) {
+      constexpr int FMT = decltype(f)::value;
+      uint32_t* scr = nullptr;
+      const int32_t rc = scratch_address(&scr);
+      if (rc != 0) return rc;
+      const bool vec_ok = host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
+      if (vec_ok) {
+        const unsigned gp = flat_grid(total / C::VEC, kPartialThreads * kPartialUnroll, kPartialMaxGroups);
+        fp8_tensor_partial<C, true><<<gp, kPartialThreads, 0, st>>>(x, total, scr);
+        bool aligned = false;
+        const unsigned g = tensor_cast_grid(total / C::VEC, gp, &aligned);
+        fp8_tensor_cast<C, FMT, false, true, true><<<g, kCastThreads, 0, st>>>(x, x_fp8, scale, nullptr, 0.0f, total,
+                                                                                aligned, scr, (int)gp);
+      } else {
+        const unsigned gp = flat_grid(total, kPartialThreads * 16, kPartialMaxGroups);
+        fp8_tensor_partial<C, false><<<gp, kPartialThreads, 0, st>>>(x, total, scr);
+        const unsigned g = flat_grid(total / C::VEC, 256, 2048);
+        fp8_tensor_cast<C, FMT, false, false, true><<<g, 256, 0, st>>>(x, x_fp8, scale, nullptr, 0.0f, total, false,
+                                                                        scr, (int)gp);
       }
       return launch_status();
     });

@@ -88,6 +88,17 @@ int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, float* scale,
 int32_t launch_fp8_quant_token_fwd(const void* x, uint8_t* x_fp8, float* scale, int64_t m,
                                    int64_t n, int32_t dtype, int32_t fp8_format, void* stream);
 
+/* As launch_fp8_quant_tensor_fwd (same codes and scale), with no caller
+ * memory beyond x, x_fp8 and scale: no counterpart in the reference. For
+ * callers that cannot allocate (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc); it calls no allocating routine. The
+ * per-workgroup maxima live in a 2048-byte device array owned by the library,
+ * one per GPU, held until the process ends; any m * n that fits int64 works
+ * (else hipErrorInvalidValue, before any device call). Every call on a GPU
+ * shares that GPU's array, so calls that overlap on one GPU race. */
+int32_t launch_fp8_quant_tensor_noalloc_fwd(const void* x, uint8_t* x_fp8, float* scale, int64_t m,
+                                            int64_t n, int32_t dtype, int32_t fp8_format, void* stream);
+
 /* FP8 with a caller-given scale: x_fp8 = fp8(x / scale). */
 int32_t launch_fp8_quant_static_fwd(const void* x, uint8_t* x_fp8, float scale, int64_t m,
                                     int64_t n, int32_t dtype, int32_t fp8_format, void* stream);
