@@ -27,8 +27,11 @@ namespace {
 template <int TOK>
 using RopeRow = RowBuf<TOK == 1, TOK == 1 ? (kPolSC1 | kPolNT) : kBufStorePolicy>;
 
+// q / k and q_out / k_out may be the same buffers (in place), so none of
+// the four is declared __restrict__; each element is loaded before the
+// element is stored, by the same thread.
 template <class C, int CHUNKS, int TOK>
-__global__ __launch_bounds__(256) void rope_tokens(const void* __restrict__ q, const void* __restrict__ k,
+__global__ __launch_bounds__(256) void rope_tokens(const void* q, const void* k,
                                                    const float* __restrict__ cos_t,
                                                    const float* __restrict__ sin_t, void* q_out,
                                                    void* k_out, int64_t tokens, int64_t seq_len,
