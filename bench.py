@@ -5,10 +5,11 @@ op. A "step" is one launch of an op over one batch of synthetic input that is
 already resident in HBM. Each op is timed over exactly --steps launches
 captured in one HIP graph (so host-side validation and launch latency are not
 in the window), bracketed by torch.cuda.synchronize() and HIP events on the
-stream the kernels run on. Every launch of a timed run uses a different set of
-input/output buffers, rotating over enough sets that the working set is
->= 2 GiB, so no step can be served from the 256 MB Infinity Cache left warm by
-the previous one.
+stream the kernels run on, after the --warmup eager launches and untimed
+replays of the graph for 0.15 s (GPU clocks ramp up under sustained load).
+Every launch of a timed run uses a different set of input/output buffers,
+rotating over enough sets that the working set is >= 2 GiB, so no step can be
+served from the 256 MB Infinity Cache left warm by the previous one.
 
 Each op also reports "per_call": the reference's own methodology (a cache
 flush before every call, HIP events around one call through the binding, so
@@ -43,6 +44,7 @@ if ROOT not in sys.path:
 
 PEAK_GBPS = 8000.0
 ROTATE_BYTES = 2 << 30
+WARM_S = 0.15
 
 
 def _parse():
@@ -64,6 +66,21 @@ def _parse():
                    help="also run a 256 MiB device-to-device torch copy, the reference kernel "
                         "for scaling FETCH_SIZE / WRITE_SIZE counters")
     return p.parse_args()
+
+
+def _c_lib():
+    """The library's C ABI through ctypes (for entry points the Python binding
+    does not wrap: the no-allocation FP8 launcher and the HBM streams)."""
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "custom_cuda_kernals_amd", "libcustom_kernels_amd.so"))
+    fn = lib.launch_fp8_quant_tensor_noalloc_fwd
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 2 + [ctypes.c_int32] * 2 + [ctypes.c_void_p]
+    fn = lib.cck_hbm_stream
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_void_p]
+    return lib
 
 
 def _ensure_built():
@@ -125,6 +142,19 @@ def _ops(torch, native):
                   lambda b: native.fp8_quant_block_fwd(b["x"], b["q"], b["sb"], "e4m3"), m1 * n1 * 3, [m1, n1]))
     ops.append(Op("fp8_quant_tensor", "fp8_tensor_bf16_2048x4096", m1 * n1 * 3 + 8, mk1g, tensor_fp8, m1 * n1 * 3,
                   [m1, n1]))
+
+    # The same tensor granularity through the no-allocation C entry point
+    # (no amax scratch, no zero-fill; library-owned partial slots).
+    lib = _c_lib()
+
+    def tensor_noalloc(b):
+        rc = lib.launch_fp8_quant_tensor_noalloc_fwd(b["x"].data_ptr(), b["q"].data_ptr(), b["st"].data_ptr(), m1, n1,
+                                                      2, 3, torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"launch_fp8_quant_tensor_noalloc_fwd failed, hipError_t = {rc}")
+
+    ops.append(Op("fp8_quant_tensor_noalloc", "fp8_tensor_noalloc_bf16_2048x4096", m1 * n1 * 3 + 4, mk1g,
+                  tensor_noalloc, m1 * n1 * 3, [m1, n1]))
 
     # Static scale 0.05 on its own (config 5's static mode fuses it into the producers).
     m1s, n1s = 16384, 4096
@@ -263,6 +293,16 @@ def _time_op(torch, op, steps, warmup, use_graph=True, per_call=True):
     torch.cuda.current_stream().wait_stream(side)
     graph.replay()  # untimed replay: first replay uploads the graph
     torch.cuda.synchronize()
+    # Untimed replays until the GPU has been busy for WARM_S: the clocks ramp
+    # up under sustained load, and the first replays after a capture measured
+    # up to 10 % slower than the settled ones (48.2, 45.1, 44.0, 43.6 us per
+    # step for RMSNorm at config 2 on MI355X).
+    t_end = time.perf_counter() + WARM_S
+    for _ in range(1000):
+        if time.perf_counter() >= t_end:
+            break
+        graph.replay()
+        torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -287,12 +327,7 @@ def _ceilings(torch, steps, warmup):
     pattern of six config ops (cck_hbm_stream, csrc/calibrate.hip: 16-byte
     nontemporal vectors, no arithmetic), timed exactly like the ops. An op's
     fraction of the 8 TB/s peak reads against its pattern's fraction here."""
-    import ctypes
-
-    lib = ctypes.CDLL(os.path.join(ROOT, "custom_cuda_kernals_amd", "libcustom_kernels_amd.so"))
-    fn = lib.cck_hbm_stream
-    fn.restype = ctypes.c_int32
-    fn.argtypes = [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_void_p]
+    fn = _c_lib().cck_hbm_stream
     u8 = torch.uint8
     # (name, pattern, op it bounds, vectors per input stream, input streams, output bytes per vector)
     cases = [
@@ -328,6 +363,31 @@ def _ceilings(torch, steps, warmup):
     return out
 
 
+def _anchors(torch, steps, warmup):
+    """Vendor kernels with config 1's traffic, timed exactly like the ops: the
+    floor of a cold 24 MiB launch is set by launch ramp and DRAM latency, not
+    by bandwidth, so it is anchored on PyTorch's own kernels on the same GPU.
+    torch_bf16_to_fp8: `q.copy_(x)`, the elementwise bf16 -> float8_e4m3fn
+    conversion (reads 16 MiB, writes 8 MiB, exactly config 1's bytes);
+    torch_copy_16MiB: a same-dtype 16 MiB device copy (reads and writes 16 MiB)."""
+    m, n = 2048, 4096
+
+    def make_set():
+        return {"x": torch.randn(m, n, device="cuda").to(torch.bfloat16),
+                "q": torch.empty(m, n, dtype=torch.float8_e4m3fn, device="cuda"),
+                "y": torch.empty(m, n, dtype=torch.bfloat16, device="cuda")}
+
+    cases = [("torch_bf16_to_fp8", lambda b: b["q"].copy_(b["x"]), m * n * 3),
+             ("torch_copy_16MiB", lambda b: b["y"].copy_(b["x"]), m * n * 4)]
+    out = {}
+    for name, launch, nbytes in cases:
+        op = Op(name, f"{name}_2048x4096", nbytes, make_set, launch, m * n * 5, [m, n])
+        r = _time_op(torch, op, steps, warmup, per_call=False)
+        out[name] = {"bounds": "fp8_quant_token", "us": r["us"], "GB_per_s": r["GB_per_s"],
+                     "frac_of_8TBps": r["frac_of_8TBps"], "bytes": nbytes}
+    return out
+
+
 def _per_call_us(torch, op, sets, calls=30):
     """The reference's methodology (benchmarks/*_bench.py, examples/llama_block.py:220-250):
     a 512 MiB write between calls so nothing is cache-resident, then HIP events
@@ -350,39 +410,88 @@ def _per_call_us(torch, op, sets, calls=30):
     return {"median_us": round(q(0.5), 3), "iqr_us": round(q(0.75) - q(0.25), 3), "calls": calls}
 
 
+def _cpu_time(fn, sets, budget_s: float):
+    """Median wall time (s) of fn(*set) over rotating input sets, ~budget_s."""
+    for i in range(min(2, len(sets))):
+        fn(*sets[i])
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter_ns()
+        fn(*sets[len(times) % len(sets)])
+        times.append(time.perf_counter_ns() - t0)
+    times.sort()
+    return times[len(times) // 2] * 1e-9, len(times)
+
+
 def _cpu_baseline(budget_s: float):
-    """Time the CPU oracle's RMSNorm+residual (torch-CPU eager restatement) on
-    a bounded row sample of the config-2 workload."""
+    """The CPU oracle (torch-CPU / numpy restatements of the reference's eager
+    baselines) timed on this host's cores, each op on a bounded row sample of
+    its config's workload, rotating over distinct inputs larger than any
+    host's last-level cache so that (like the GPU timing) no run is served
+    from cache. The headline is RMSNorm + residual (config 2); `per_op` holds
+    every config op."""
     import torch
 
     from oracle import eager, inputs
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    bf16 = torch.bfloat16
+
+    def rot_sets(make, set_bytes, total=256 << 20, cap=64):
+        return [make(i) for i in range(max(2, min(cap, total // set_bytes)))]
+
+    per_op = {}
+
+    def record(name, fn, sets, nbytes, sample, share):
+        med, runs = _cpu_time(fn, sets, budget_s * share)
+        per_op[name] = {"ms_per_run": round(med * 1e3, 3), "TB_per_s": round(nbytes / med / 1e12, 6),
+                        "frac_of_8TBps": round(nbytes / med / 8e12, 6), "runs": runs, "sets": len(sets),
+                        "sample": sample}
+
+    # 2: RMSNorm + residual, [1024, 4096] rows of config 2 (1 GiB rotation, the headline)
     rows, cols = 1024, 4096
-    # Rotate over 1 GiB of distinct inputs, more than any host's last-level
-    # cache, so that (like the GPU timing) no run is served from cache.
-    nsets = (1 << 30) // (rows * cols * 2 * 2)
-    x0, r0, w = inputs.rmsnorm_inputs(rows, cols, torch.bfloat16, seed=0)
-    sets = [(x0.roll(i, 0), r0.roll(-i, 0), w) for i in range(nsets)]  # distinct copies, same distribution
-    for i in range(2):
-        eager.rmsnorm_residual(*sets[i], 1e-5)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 5:
-        x, r, w = sets[len(times) % nsets]
-        t0 = time.perf_counter_ns()
-        eager.rmsnorm_residual(x, r, w, 1e-5)
-        times.append(time.perf_counter_ns() - t0)
+    x0, r0, w = inputs.rmsnorm_inputs(rows, cols, bf16, seed=0)
+    sets = [(x0.roll(i, 0), r0.roll(-i, 0), w, 1e-5) for i in range((1 << 30) // (rows * cols * 4))]
+    record("rmsnorm_residual", eager.rmsnorm_residual, sets, rows * cols * 8 + cols * 2,
+           f"eager rmsnorm_residual, bf16 [{rows},{cols}]", 0.45)
     del sets
-    times.sort()
-    med_s = times[len(times) // 2] * 1e-9
-    nbytes = rows * cols * 8 + cols * 2
-    return {"value": round(nbytes / med_s / 1e12, 6), "unit": "TB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+    # 1: per-token FP8 with torch's CPU cast, [512, 4096] rows of the config-1 input
+    xt = inputs.fp8_token_input(2048, 4096, bf16, seed=0)
+    sets = rot_sets(lambda i: (xt[(i % 4) * 512:(i % 4 + 1) * 512].roll(i, 1).contiguous(), "e4m3"),
+                    512 * 4096 * 2)
+    record("fp8_quant_token", eager.fp8_quant_token_torch, sets, 512 * 4096 * 3 + 512 * 4,
+           "eager per-row fp8 quant (torch cast), bf16 [512,4096] rows of the config-1 input", 0.1)
+    del sets, xt
+    # 3: SwiGLU, [256, 14336] rows of config 3
+    sets = rot_sets(lambda i: inputs.swiglu_inputs(256, 14336, bf16, seed=i), 256 * 14336 * 4, cap=16)
+    record("swiglu", eager.swiglu, sets, 256 * 14336 * 6, "eager swiglu, bf16 [256,14336]", 0.1)
+    # 3v: SwiGLU + per-token FP8 (composition), same rows
+    record("swiglu_fp8_token", lambda g, u: eager.fp8_quant_token_torch(eager.swiglu(g, u)), sets,
+           256 * 14336 * 5 + 256 * 4, "eager swiglu then per-row fp8 quant (torch cast), bf16 [256,14336]", 0.1)
+    del sets
+    # 4: RoPE, q [1,512,32,128] + k [1,512,8,128] of config 4 (theta 5e5)
+    cos, sin = eager.compute_cos_sin(512, 128, inputs.ROPE_THETA)
+    sets = rot_sets(lambda i: inputs.rope_inputs(1, 512, 32, 8, 128, bf16, seed=i)[:2] + (cos, sin),
+                    512 * 40 * 128 * 2, cap=16)
+    record("rope", eager.rope, sets, 512 * 40 * 128 * 4, "eager rope, q [1,512,32,128] + k [1,512,8,128] bf16", 0.1)
+    del sets
+    # 5a: RMSNorm + residual + per-token FP8 (composition), [512, 4096] rows of config 5
+    x5, r5, w5 = inputs.rmsnorm_inputs(512, 4096, bf16, seed=1)
+    sets = [(x5.roll(i, 0), r5.roll(-i, 0), w5, 1e-5) for i in range(16)]
+    record("rmsnorm_residual_fp8_token",
+           lambda x, r, w, eps: eager.fp8_quant_token_torch(eager.rmsnorm_residual(x, r, w, eps)[0]),
+           sets, 512 * 4096 * 7 + 512 * 4 + 4096 * 2,
+           "eager rmsnorm_residual then per-row fp8 quant (torch cast), bf16 [512,4096]", 0.15)
+    del sets
+
+    head = per_op["rmsnorm_residual"]
+    return {"value": head["TB_per_s"], "unit": "TB/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"oracle eager rmsnorm_residual on bf16 [{rows},{cols}] rows of the config-2 workload, "
-                      f"rotating over {nsets} distinct input sets (1 GiB, so not cache-resident), "
-                      f"median of {len(times)} runs over ~{budget_s:.0f}s, {med_s * 1e3:.3f} ms/run"}
+                      f"rotating over 1 GiB of distinct inputs, median of {head['runs']} runs, "
+                      f"{head['ms_per_run']:.3f} ms/run; per_op: every config op's oracle on a row sample",
+            "per_op": per_op}
 
 
 def _block_latency(torch):
@@ -456,6 +565,15 @@ def main():
             if done:
                 c["op_frac_of_ceiling"] = round(done["GB_per_s"] / c["GB_per_s"], 4)
             print(f"# ceiling {name}: {c}", file=sys.stderr, flush=True)
+    anchors = None
+    if not args.no_ceilings and not args.no_graph:
+        anchors = _anchors(torch, args.steps, args.warmup)
+        for name, a in anchors.items():
+            done = results.get(a["bounds"])
+            if done:
+                a["op_frac_of_anchor_bandwidth"] = round(done["GB_per_s"] / a["GB_per_s"], 4)
+                a["op_speedup_over_anchor"] = round(a["us"] / done["us"], 4)
+            print(f"# anchor {name}: {a}", file=sys.stderr, flush=True)
     if args.copy_calibration:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -488,6 +606,8 @@ def main():
     }
     if ceilings:
         line["ceilings"] = ceilings
+    if anchors:
+        line["anchors"] = anchors
     if args.block:
         line["block"] = _block_latency(torch)
     if not args.no_cpu_baseline:

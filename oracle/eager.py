@@ -90,6 +90,25 @@ def rope_fp64(q, k, cos, sin):
     return rot(q), rot(k)
 
 
+# --- per-token FP8 with torch's own CPU cast ----------------------------------
+
+_FP8_TORCH = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+
+
+def fp8_quant_token_torch(x: torch.Tensor, fmt: str = "e4m3"):
+    """eager_fp8_quant's "tensor" formula (baselines/fp8_quant.py:162-178)
+    applied per row of a [M, N] tensor with torch's CPU ops: amax, clamp(amax /
+    FP8_MAX, min=1e-12), (x.float() / scale).to(fp8). Returns (codes as uint8
+    [M, N], scale [M]). The CPU baseline times this (torch's cast, as the
+    reference's eager path runs); oracle.fp8.quant_token is the exact-encoder
+    restatement it is pinned against (tests/test_oracle_fp8.py)."""
+    dt = _FP8_TORCH[fmt]
+    x32 = x.to(torch.float32)
+    amax = x32.abs().amax(dim=-1, keepdim=True)
+    scale = torch.clamp(amax / torch.finfo(dt).max, min=1e-12)
+    return (x32 / scale).to(dt).view(torch.uint8), scale.reshape(-1)
+
+
 # --- fused compositions -------------------------------------------------------
 
 def to_f32_numpy(t: torch.Tensor) -> np.ndarray:

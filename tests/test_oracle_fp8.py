@@ -181,3 +181,19 @@ def test_block_scales_keep_a_small_tile_resolved_next_to_an_outlier_tile():
     err_b = np.abs(deq_b[:128, :128] - small).mean()
     assert err_b * 2 < err_t, (err_b, err_t)
     assert err_b < 0.04 * np.abs(small).mean()  # within e4m3's relative step
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_torch_per_token_restatement_equals_exact_encoder(fmt):
+    """oracle.eager.fp8_quant_token_torch (torch's own cast, timed by the CPU
+    baseline) gives the same codes and scales as oracle.fp8.quant_token, on
+    rows with outliers, a zero row and signed zeros."""
+    from oracle import eager, inputs
+
+    x = inputs.fp8_token_input(64, 4096, torch.bfloat16, seed=2)
+    x[3] = 0.0
+    x[5, ::2] = -0.0
+    codes_t, scale_t = eager.fp8_quant_token_torch(x, fmt)
+    codes, scale = fp8.quant_token(x.float().numpy(), fmt)
+    np.testing.assert_array_equal(codes_t.numpy(), codes)
+    np.testing.assert_array_equal(scale_t.numpy().view(np.uint32), scale.view(np.uint32))
