@@ -380,10 +380,11 @@ __global__ __launch_bounds__(VECTOR ? kCastThreads : 256) void fp8_tensor_cast(
     // workgroups (the partial's grid a multiple of 8, this one a multiple
     // of 16), workgroup 8a + c re-reads a half of partial chunk
     // 8 (a / 2) + c: workgroups are dealt to the 8 XCDs round-robin, so
-    // that half was read by the same XCD and is still in its L2 (12.4-12.7
-    // vs 13.4-13.6 us for the whole reference-ABI op at [2048, 4096] bf16 on
-    // MI355X). Otherwise the chunks are walked last-first, starting on the
-    // most recently read part of x.
+    // that half is re-read by the XCD that read it (12.4-12.7 vs 13.4-13.6 us
+    // for the whole reference-ABI op at [2048, 4096] bf16 on MI355X; the
+    // FETCH_SIZE counter shows the re-read still leaves the L2, so the gain
+    // is on the path beyond it). Otherwise the chunks are walked last-first,
+    // starting on the most recently read part of x.
     if (xcd_aligned) {
       const int64_t a = blockIdx.x / 8, c = blockIdx.x % 8;
       bid = 2 * (8 * (a / 2) + c) + (a % 2);
