@@ -17,6 +17,7 @@
 // whose scale is non-finite, or whose quotients leave the verified range of
 // the hardware conversion, take the exact path (x86-compatible division +
 // software encoder) as a workgroup-uniform branch.
+#include <atomic>
 #include <mutex>
 
 #include "launch.hpp"
@@ -475,19 +476,155 @@ int32_t launch_token(const void* x, uint8_t* q, float* scale, int64_t m, int64_t
 // ---------------------------------------------------------------------------
 // Tensor granularity with no memory from the caller beyond the input and the
 // outputs (no counterpart in the reference; for callers that cannot allocate:
-// code under HIP graph capture, serving loops). The partial maxima live in
-// `scratch`, a file-scope device array of kPartialMaxGroups words (2 KiB):
-// the partial pass runs at most kPartialMaxGroups workgroups for any input
-// size, so every size fits, and every cast workgroup reduces the slots
-// itself, so no finishing kernel runs and nothing needs clearing (each call
-// writes every slot it reads). Every call on a device shares that device's
+// code under HIP graph capture, serving loops). Its state lives in `scratch`,
+// a file-scope device array of kScratchWords words (6.5 KiB), one per GPU,
+// held until the process ends. Every call on a device shares that device's
 // array: calls that overlap on one GPU (on different streams) race.
+//
+// Inputs that fit in the registers of a grid that is resident at once take
+// fp8_tensor_onepass: x is read from HBM once and the op is one launch. The
+// others take the two-pass form above, with the partial maxima in the slots
+// and every cast workgroup reducing them itself (each call writes every slot
+// it reads, so nothing needs clearing).
+//
+// fp8_tensor_onepass: each workgroup keeps its share of x in registers,
+// stores its max |x| bits into its slot, and arrives at the counter of its
+// group (workgroup b is in group b % 8; workgroups are dealt to the 8 XCDs
+// round-robin, so a group is one XCD's share). The last arrival of a group
+// resets that counter and arrives at the top counter; the last arrival there
+// resets it, reduces the slots and publishes {generation + 1, amax bits} in
+// the result word. Every other workgroup polls the result word until its
+// generation moves past the one it read before arriving, then converts what
+// it holds. Counters return to zero in every call and the generation only
+// moves forward, so no call needs memory cleared.
+//
+// Every word shared between workgroups is read and written only by
+// agent-scope atomics, which gfx950 performs beyond the per-XCD L2s, and a
+// workgroup waits for its slot store to complete before it arrives. That wait
+// is the ordering an agent-scope release gives atomic data; the release's L2
+// writeback and the acquire's L2 invalidation serve only non-atomic data and
+// are left out (6.8-6.9 vs 8.5-9.9 us per launch for the exchange at
+// [2048, 4096] bf16 on MI355X).
+//
+// Waiting needs the whole grid resident at once: the launcher sizes the grid
+// to the occupancy the runtime reports for the device. A workgroup whose wait
+// still runs past the poll limit (other work holding CUs) reads all of x and
+// takes the maximum itself, so the result never depends on residency.
 // ---------------------------------------------------------------------------
-static __device__ __align__(256) uint32_t scratch[kPartialMaxGroups];
+constexpr int kOnePassThreads = 1024, kOnePassMaxGroups = 1024;
+constexpr int kLineWords = 64;  // counters and the result word each own a 256-byte line
+constexpr int kGroupCounter = kOnePassMaxGroups;                  // + group * kLineWords, group < 8
+constexpr int kTopCounter = kGroupCounter + 8 * kLineWords;
+constexpr int kResultWord = kTopCounter + kLineWords;             // 64-bit {generation, amax bits}
+constexpr int kScratchWords = kResultWord + kLineWords;
+static_assert(kOnePassMaxGroups >= kPartialMaxGroups, "the two-pass form's partial maxima use the same slots");
+static_assert(kResultWord % 2 == 0, "the result word is 8-byte aligned");
+
+static __device__ __align__(256) uint32_t scratch[kScratchWords];
+
+__device__ inline uint32_t agent_load(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t agent_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ inline void agent_store(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint32_t agent_add(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this thread's memory operations have completed (s_waitcnt with
+// every counter at zero); the compiler moves no memory access across it.
+__device__ inline void wait_memory_ops() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// U 16-byte vectors per thread; requires 16-byte aligned x, VEC-aligned q,
+// total % VEC == 0 and gridDim.x <= kOnePassMaxGroups, all resident at once.
+template <class C, int FMT, int U>
+__global__ __launch_bounds__(kOnePassThreads) void fp8_tensor_onepass(const void* __restrict__ x,
+                                                                      uint8_t* __restrict__ q,
+                                                                      float* __restrict__ scale_out, int64_t nvec,
+                                                                      uint32_t* __restrict__ sync, int poll_limit) {
+  constexpr int T = kOnePassThreads, NW = T / 64;
+  __shared__ uint32_t lds[2 * NW];
+  __shared__ uint32_t last_s, late_s, amax_s;
+  const u32x4* xv = static_cast<const u32x4*>(x);
+  uint64_t* result = reinterpret_cast<uint64_t*>(sync + kResultWord);
+  uint32_t gen = 0;
+  if (threadIdx.x == 0) gen = (uint32_t)(agent_load(result) >> 32);
+  const int64_t b0 = (int64_t)blockIdx.x * T * U + threadIdx.x;
+  u32x4 raw[U];
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    if (b0 + k * T < nvec) raw[k] = ld_stream(xv + b0 + k * T);
+  }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    if (b0 + k * T < nvec) acc = C::absmax_vec(raw[k], acc);
+  }
+  acc = block_allreduce<NW>(acc, typename AmaxOp<C>::type{}, lds, 0);
+  if (threadIdx.x == 0) {
+    agent_store(sync + blockIdx.x, f32_bits(C::absmax_to_float(acc)));
+    wait_memory_ops();
+    const unsigned g = gridDim.x, c = blockIdx.x % 8;
+    uint32_t* group = sync + kGroupCounter + c * kLineWords;
+    bool last = agent_add(group, 1u) == (g - c + 7) / 8 - 1;
+    if (last) {
+      agent_store(group, 0u);
+      last = agent_add(sync + kTopCounter, 1u) == min(g, 8u) - 1;
+      if (last) agent_store(sync + kTopCounter, 0u);
+    }
+    last_s = last;
+  }
+  __syncthreads();
+  uint32_t amax_bits;
+  if (last_s) {
+    uint32_t m = 0;
+    for (unsigned i = threadIdx.x; i < gridDim.x; i += T) m = max(m, agent_load(sync + i));
+    amax_bits = block_allreduce<NW>(m, MaxU32{}, lds, 1);
+    if (threadIdx.x == 0) agent_store(result, ((uint64_t)(gen + 1) << 32) | amax_bits);
+  } else {
+    if (threadIdx.x == 0) {
+      uint64_t w = agent_load(result);
+      for (int i = 0; (uint32_t)(w >> 32) == gen && i < poll_limit; ++i) {
+        __builtin_amdgcn_s_sleep(2);
+        w = agent_load(result);
+      }
+      amax_s = (uint32_t)w;
+      late_s = (uint32_t)(w >> 32) == gen;
+    }
+    __syncthreads();
+    amax_bits = amax_s;
+    if (late_s) {
+      // The wait ran past its limit: the maximum over all of x, read by this workgroup.
+      uint32_t a = 0;
+      for (int64_t v = threadIdx.x; v < nvec; v += T) a = C::absmax_vec(ld_stream(xv + v), a);
+      amax_bits = f32_bits(C::absmax_to_float(block_allreduce<NW>(a, typename AmaxOp<C>::type{}, lds, 1)));
+    }
+  }
+  const float amax_t = bits_f32(amax_bits);
+  const float s = scale_from_amax<FMT>(amax_t);
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
+  const float r = 1.0f / s;
+  const bool fast = fast_path_ok<FMT>(s, r, amax_t);
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const int64_t v = b0 + k * T;
+    if (v < nvec) quant_vec<C, FMT>(raw[k], s, r, fast, q, v * C::VEC);
+  }
+}
 
 constexpr int kMaxDevices = 64;
+constexpr int kDefaultPollLimit = 1 << 16;  // polls of about 1 us each before a workgroup reads x itself
 std::mutex scratch_mu;
 uint32_t* scratch_dev[kMaxDevices] = {};
+std::atomic<int> poll_limit{kDefaultPollLimit};
 
 // The current device's address of `scratch`, looked up once per device. The
 // host-side name of the array is only a handle for the runtime: kernels are
@@ -506,6 +643,47 @@ int32_t scratch_address(uint32_t** out) {
   }
   *out = scratch_dev[dev];
   return (int32_t)hipSuccess;
+}
+
+// Workgroups of fp8_tensor_onepass<C, FMT, U> the current device holds at
+// once (occupancy per CU x CUs, at most kOnePassMaxGroups; 0 if unknown).
+template <class C, int FMT, int U>
+int onepass_groups() {
+  static int groups[kMaxDevices] = {};  // per instantiation; -1 = the query failed
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (groups[dev] == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fp8_tensor_onepass<C, FMT, U>, kOnePassThreads, 0) !=
+            hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      groups[dev] = -1;
+    } else {
+      groups[dev] = per_cu * cus > 0 ? std::min(per_cu * cus, kOnePassMaxGroups) : -1;
+    }
+  }
+  return std::max(groups[dev], 0);
+}
+
+// Launches fp8_tensor_onepass with the fewest vectors per thread (U = 1, 2, 4
+// or 8) whose grid the device holds at once; false if none does.
+template <class C, int FMT>
+bool launch_onepass(const void* x, uint8_t* q, float* scale, int64_t nvec, uint32_t* sync, hipStream_t st) {
+  const int polls = poll_limit.load(std::memory_order_relaxed);
+  auto attempt = [&](auto u) {
+    constexpr int U = decltype(u)::value;
+    const int64_t per_group = (int64_t)kOnePassThreads * U;
+    const int64_t g = (nvec + per_group - 1) / per_group;
+    if (g > onepass_groups<C, FMT, U>()) return false;
+    fp8_tensor_onepass<C, FMT, U><<<(unsigned)g, kOnePassThreads, 0, st>>>(x, q, scale, nvec, sync, polls);
+    return true;
+  };
+  return attempt(IntC<1>{}) || attempt(IntC<2>{}) || attempt(IntC<4>{}) || attempt(IntC<8>{});
 }
 
 }  // namespace
@@ -644,6 +822,9 @@ extern "C" int32_t launch_fp8_quant_tensor_noalloc_fwd(const void* x, uint8_t* x
       const int32_t rc = scratch_address(&scr);
       if (rc != 0) return rc;
       const bool vec_ok = host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
+      if (vec_ok && total % C::VEC == 0 && launch_onepass<C, FMT>(x, x_fp8, scale, total / C::VEC, scr, st)) {
+        return launch_status();
+      }
       if (vec_ok) {
         const unsigned gp = flat_grid(total / C::VEC, kPartialThreads * kPartialUnroll, kPartialMaxGroups);
         fp8_tensor_partial<C, true><<<gp, kPartialThreads, 0, st>>>(x, total, scr);
@@ -661,4 +842,8 @@ extern "C" int32_t launch_fp8_quant_tensor_noalloc_fwd(const void* x, uint8_t* x
       return launch_status();
     });
   });
+}
+
+extern "C" int32_t cck_fp8_tensor_noalloc_poll_limit(int32_t polls) {
+  return polls < 0 ? cck::poll_limit.load() : cck::poll_limit.exchange(polls);
 }

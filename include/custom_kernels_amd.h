@@ -91,11 +91,13 @@ int32_t launch_fp8_quant_token_fwd(const void* x, uint8_t* x_fp8, float* scale, 
 /* As launch_fp8_quant_tensor_fwd (same codes and scale), with no caller
  * memory beyond x, x_fp8 and scale: no counterpart in the reference. For
  * callers that cannot allocate (code under HIP graph capture, serving loops,
- * harnesses that forbid hipMalloc); it calls no allocating routine. The
- * per-workgroup maxima live in a 2048-byte device array owned by the library,
- * one per GPU, held until the process ends; any m * n that fits int64 works
- * (else hipErrorInvalidValue, before any device call). Every call on a GPU
- * shares that GPU's array, so calls that overlap on one GPU race. */
+ * harnesses that forbid hipMalloc); it calls no allocating routine. Its
+ * per-workgroup maxima and arrival counters live in a 6656-byte device array
+ * owned by the library, one per GPU, held until the process ends; any m * n
+ * that fits int64 works (else hipErrorInvalidValue, before any device call).
+ * An input that fits in the registers of a grid the GPU holds at once is
+ * read once, in one launch. Every call on a GPU shares that GPU's array, so
+ * calls that overlap on one GPU race. */
 int32_t launch_fp8_quant_tensor_noalloc_fwd(const void* x, uint8_t* x_fp8, float* scale, int64_t m,
                                             int64_t n, int32_t dtype, int32_t fp8_format, void* stream);
 
@@ -189,6 +191,13 @@ int32_t cck_scale_selftest(uint64_t start, uint64_t count, int32_t fp8_format,
  * UINT64_MAX; [0], [1], [3] are mismatch counts; see csrc/selftest.hip for the
  * layout. */
 int32_t cck_silu_table_selftest(unsigned long long* counters, void* stream);
+
+/* Test hook (no reference counterpart): sets the number of polls a
+ * workgroup of the one-pass launch_fp8_quant_tensor_noalloc_fwd makes for the
+ * device-wide maximum before it reads all of x and takes the maximum itself
+ * (default 65536); polls < 0 only queries. Returns the previous value. Takes
+ * effect for later launches. */
+int32_t cck_fp8_tensor_noalloc_poll_limit(int32_t polls);
 
 /* HBM calibration stream (no reference counterpart): one launch of a pure
  * traffic pattern on 16-byte nontemporal vectors, to measure the practical

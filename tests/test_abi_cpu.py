@@ -301,3 +301,14 @@ int main(void) {
                     "-lcustom_kernels_amd", f"-Wl,-rpath,{lib_dir}", "-o", str(exe)], check=True)
     run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert run.returncode == 0 and run.stdout.strip() == "OK", run.stdout + run.stderr
+
+
+def test_noalloc_poll_limit_hook_is_host_state():
+    """The one-pass per-tensor kernel's poll limit: a host-side setting (no
+    device call), default 65536, returned on change and restorable."""
+    lib = _cck.load()
+    prev = lib.cck_fp8_tensor_noalloc_poll_limit(-1)
+    assert prev == 65536
+    assert lib.cck_fp8_tensor_noalloc_poll_limit(17) == prev
+    assert lib.cck_fp8_tensor_noalloc_poll_limit(-1) == 17
+    assert lib.cck_fp8_tensor_noalloc_poll_limit(prev) == 17

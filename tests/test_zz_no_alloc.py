@@ -4,6 +4,13 @@ oracle (baselines/fp8_quant.py:162-178 with one scale for the tensor), bit
 for bit: codes and scale. Two calls in a row, the second on a smaller input,
 so the second call starts from the array as the first left it; plus the
 scalar (unaligned) path, both formats and every input dtype.
+
+Inputs that fit in the registers of a resident grid take the one-pass kernel
+(a device-wide exchange of workgroup maxima through counters and a result
+word in the array); the rest take the two-pass form. Both are covered, with
+calls of either kind queued back to back, and the one-pass kernel's fallback
+(a workgroup whose wait runs out reads all of x itself) is forced from the
+host with a poll limit of zero.
 """
 
 from __future__ import annotations
@@ -117,6 +124,67 @@ def test_back_to_back_without_synchronising():
         codes, s_oracle = ofp8.quant_tensor(x.float().numpy(), "e4m3")
         assert_codes_equal(q, codes)
         assert_f32_bits_equal(s, s_oracle)
+
+
+@pytest.mark.parametrize("shape", [(4096, 8192), (4097, 8192)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_register_capacity_boundary(shape):
+    """[4096, 8192] bf16 is 8 vectors per thread over 512 workgroups of 1024
+    threads (one pass when the GPU holds 512 at once); one more row is two passes."""
+    x = inputs.randn(shape, torch.bfloat16, seed=shape[0])
+    x.view(-1)[-5] = 900.0
+    _check_pair(x, "e4m3")
+
+
+def test_mixed_sequence_queued_without_synchronising():
+    """One-pass grids of 1, 7, 8, 9, 64 and 512 workgroups (the exchange's
+    group and top counters at every fill), a two-pass input between them and
+    an unaligned one, all queued on one stream before any result is read."""
+    shapes = [(1, 8), (7, 1024 * 8), (8, 1024 * 8), (9, 1024 * 8), (64, 1024 * 8), (2048, 4096), (8193, 8192),
+              (3, 1030), (2048, 4096), (1, 8), (100, 4096)]
+    xs = [inputs.randn(s, torch.bfloat16, seed=40 + i) * (0.5 + i) for i, s in enumerate(shapes)]
+    for i, x in enumerate(xs):
+        x.view(-1)[(i * 7919) % x.numel()] = -(3.0 + 50 * i)
+    outs = []
+    for x in xs:
+        q = torch.empty(x.shape, dtype=torch.uint8, device="cuda")
+        outs.append((q, _noalloc(x.cuda(), q, "e4m3")))
+    torch.cuda.synchronize()
+    for x, (q, s) in zip(xs, outs):
+        codes, s_oracle = ofp8.quant_tensor(x.float().numpy(), "e4m3")
+        assert_codes_equal(q, codes)
+        assert_f32_bits_equal(s, s_oracle)
+
+
+def test_special_values_take_the_exact_path():
+    """inf and NaN in a one-pass input: the scale is non-finite, every code
+    comes from the exact encoder, as in the reference-ABI launcher."""
+    for val in (float("inf"), float("nan")):
+        x = inputs.randn((256, 4096), torch.bfloat16, seed=61)
+        x.view(-1)[12345] = val
+        x_dev = x.cuda()
+        q = torch.empty(x.shape, dtype=torch.uint8, device="cuda")
+        scale = _noalloc(x_dev, q, "e4m3")
+        q_ref, s_ref = _reference_abi(x_dev, "e4m3")
+        torch.cuda.synchronize()
+        assert torch.equal(q.cpu(), q_ref.cpu())
+        assert_f32_bits_equal(scale, s_ref.cpu().numpy())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+def test_wait_fallback_reads_x_itself(dtype):
+    """Poll limit 0: every workgroup but the last arrival stops waiting at
+    once and takes the maximum over all of x itself; the results are the same
+    bits, and the exchange state stays consistent for the calls after it."""
+    lib = _lib()
+    prev = lib.cck_fp8_tensor_noalloc_poll_limit(0)
+    try:
+        assert lib.cck_fp8_tensor_noalloc_poll_limit(-1) == 0
+        _check_pair(inputs.randn((2048, 4096), dtype, seed=71) * 3, "e4m3")
+        _check_pair(inputs.randn((24, 4096), dtype, seed=72), "e5m2")
+    finally:
+        assert lib.cck_fp8_tensor_noalloc_poll_limit(prev) == 0
+    assert lib.cck_fp8_tensor_noalloc_poll_limit(-1) == prev
+    _check_pair(inputs.randn((2048, 4096), dtype, seed=73), "e4m3")
 
 
 def test_rejects_size_beyond_int64_before_device_calls():
