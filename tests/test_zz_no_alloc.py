@@ -187,6 +187,52 @@ def test_wait_fallback_reads_x_itself(dtype):
     _check_pair(inputs.randn((2048, 4096), dtype, seed=73), "e4m3")
 
 
+def test_graph_replays_with_eager_calls_between():
+    """The entry point captured in a HIP graph (two calls: a one-pass size and
+    a two-pass size), replayed with new inputs copied into the captured
+    buffers and poisoned outputs; eager calls of other sizes run between the
+    replays and move the array's state on. Every replay equals the reference
+    ABI on the same inputs, bit for bit."""
+    shapes = [(2048, 4096), (8193, 8192)]
+    dev_in = [torch.empty(s, dtype=torch.bfloat16, device="cuda") for s in shapes]
+    dev_q = [torch.empty(s, dtype=torch.uint8, device="cuda") for s in shapes]
+    dev_s = [torch.empty(1, dtype=torch.float32, device="cuda") for _ in shapes]
+    stream_of = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def launch():
+        for x, q, sc in zip(dev_in, dev_q, dev_s):
+            m, n = x.shape
+            assert _lib().launch_fp8_quant_tensor_noalloc_fwd(x.data_ptr(), q.data_ptr(), sc.data_ptr(), m, n, 2, 3,
+                                                               stream_of()) == 0
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        xs = [inputs.randn(s, torch.bfloat16, seed=90 + 3 * rep + i) * (1 + rep) for i, s in enumerate(shapes)]
+        for d, x in zip(dev_in, xs):
+            d.copy_(x)
+        for q, sc in zip(dev_q, dev_s):
+            q.fill_(0x5A)
+            sc.fill_(float("nan"))
+        # eager calls of other sizes between the replays
+        _check_pair(inputs.randn((64 * (rep + 1), 4096), torch.bfloat16, seed=80 + rep), "e4m3")
+        graph.replay()
+        torch.cuda.synchronize()
+        for d, q, sc in zip(dev_in, dev_q, dev_s):
+            q_ref, s_ref = _reference_abi(d, "e4m3")
+            torch.cuda.synchronize()
+            assert torch.equal(q.cpu(), q_ref.cpu()), f"replay {rep}: codes differ for {tuple(d.shape)}"
+            assert_f32_bits_equal(sc, s_ref.cpu().numpy())
+
+
 def test_rejects_size_beyond_int64_before_device_calls():
     lib = _lib()
     assert lib.launch_fp8_quant_tensor_noalloc_fwd(None, None, None, 1 << 40, 1 << 40, 2, 3, None) == 1
