@@ -172,7 +172,20 @@ def _bench_rows(line: dict) -> list[tuple[str, dict]]:
     return list(line.get("ops", {}).items())
 
 
-def _bench_table(spec: OpSpec, line: dict) -> None:
+def _bench_table(spec: OpSpec, line: dict, full: bool = False) -> None:
+    if full:  # every recorded field, one table per bench.py op
+        for name, r in _bench_rows(line):
+            t = Table(title=name, box=box.SIMPLE_HEAVY, header_style="bold cyan")
+            t.add_column("field")
+            t.add_column("value", justify="right", overflow="fold")
+            for k, v in r.items():
+                if isinstance(v, dict):
+                    for k2, v2 in v.items():
+                        t.add_row(f"{k}.{k2}", str(v2))
+                else:
+                    t.add_row(k, str(v))
+            console.print(t)
+        return
     t = Table(title=f"{spec.id} (bench.py)", box=box.SIMPLE_HEAVY, header_style="bold cyan")
     for c in ("op", "workload", "µs / launch", "GB/s", "of 8 TB/s", "per call µs (flush, binding)"):
         t.add_column(c, justify="left" if c in ("op", "workload") else "right",
@@ -186,18 +199,24 @@ def _bench_table(spec: OpSpec, line: dict) -> None:
 
 @app.command()
 def benchmark(op: str = typer.Argument(..., help="Op id (see `list`)."),
+              rerun: bool = typer.Option(False, "--rerun", help="Run bench.py even if a result is stored."),
+              full: bool = typer.Option(False, "--full", help="Show every recorded field, not just the key ones."),
               steps: int = typer.Option(100, "--steps", help="Timed launches per bench.py op."),
               timeout: int = typer.Option(900, "--timeout", help="Max seconds for bench.py.")) -> None:
-    """Run bench.py for the op (graph-replayed, >= 2 GiB buffer rotation)."""
+    """Run bench.py for the op (graph-replayed, >= 2 GiB buffer rotation), or show its stored result."""
     spec = _resolve(op)
-    _require_gpu()
-    with console.status(f"[cyan]bench.py --ops {','.join(spec.bench_ops)}...[/cyan]"):
-        try:
-            line = run_bench(spec.id, spec.bench_ops, steps, timeout)
-        except Exception as e:
-            err.print(f"[bold red]{e}[/bold red]")
-            raise typer.Exit(code=1) from e
-    _bench_table(spec, line)
+    line = None if rerun else load_bench(spec.id)
+    if line is None:
+        _require_gpu()
+        with console.status(f"[cyan]bench.py --ops {','.join(spec.bench_ops)}...[/cyan]"):
+            try:
+                line = run_bench(spec.id, spec.bench_ops, steps, timeout)
+            except Exception as e:
+                err.print(f"[bold red]{e}[/bold red]")
+                raise typer.Exit(code=1) from e
+    else:
+        console.print(f"[dim]stored result (cli_results/bench_{spec.id}.json); --rerun measures again[/dim]")
+    _bench_table(spec, line, full)
 
 
 @app.command()
@@ -258,6 +277,7 @@ def visualize(op: str = typer.Argument(..., help="Op id (see `list`)."),
 
 @app.command()
 def profile(op: str = typer.Argument(..., help="Op id (see `list`)."),
+            warmup: int = typer.Option(5, "--warmup", help="Calls before the profiled ones."),
             iters: int = typer.Option(10, "--iters", help="Profiled calls."),
             output: Path | None = typer.Option(None, "--output", "-o", help="Output directory."),  # noqa: B008
             timeout: int = typer.Option(600, "--timeout", help="Max seconds for rocprofv3.")) -> None:
@@ -265,9 +285,9 @@ def profile(op: str = typer.Argument(..., help="Op id (see `list`)."),
     spec = _resolve(op)
     _require_gpu()
     out = output or (RESULTS / f"profile_{spec.id}_{time.strftime('%Y%m%d_%H%M%S')}")
-    with console.status(f"[cyan]rocprofv3 --kernel-trace --stats over {iters} calls...[/cyan]"):
+    with console.status(f"[cyan]rocprofv3 --kernel-trace --stats over {warmup} + {iters} calls...[/cyan]"):
         try:
-            r = run_profile(spec.id, iters, out, timeout)
+            r = run_profile(spec.id, iters, out, timeout, warmup=warmup)
         except Exception as e:
             err.print(f"[bold red]{e}[/bold red]")
             raise typer.Exit(code=1) from e
@@ -279,3 +299,5 @@ def profile(op: str = typer.Argument(..., help="Op id (see `list`)."),
         t.add_row(*[(row[c][:90] if c == "Name" else row[c]) for c in cols])
     console.print(t)
     console.print(f"{OK} trace and statistics in {r.out_dir}")
+    if r.trace is not None:
+        console.print(f"[dim]Timeline: {r.trace} (open in https://ui.perfetto.dev).[/dim]")

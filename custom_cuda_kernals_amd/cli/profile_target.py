@@ -1,5 +1,5 @@
-"""The program `profile` runs under rocprofv3: `iters` calls of one op's
-representative kernel call (after two warm-up calls), then exit."""
+"""The program `profile` runs under rocprofv3: `warmup` calls (default 2),
+then `iters` calls of one op's representative kernel call, then exit."""
 
 from __future__ import annotations
 
@@ -16,8 +16,9 @@ def main(argv: list[str]) -> int:
         print(f"unknown op {argv[0]!r}", file=sys.stderr)
         return 2
     iters = int(argv[1]) if len(argv) > 1 else 10
+    warmup = int(argv[2]) if len(argv) > 2 else 2
     target = spec.build_target("cuda")
-    for _ in range(2):
+    for _ in range(warmup):
         target.kernel()
     torch.cuda.synchronize()
     for _ in range(iters):

@@ -111,17 +111,20 @@ def time_pair(target, iters: int = 20, warmup: int = 5) -> dict:
 class ProfileResult:
     out_dir: Path
     top: list[dict]
+    trace: Path | None  # Perfetto trace (ui.perfetto.dev), when rocprofv3 wrote one
 
 
-def run_profile(op_id: str, iters: int, out_dir: Path, timeout: int) -> ProfileResult:
-    """rocprofv3 kernel trace of `iters` calls of the op's representative
-    target (the program itself follows `--`, with no launcher in between)."""
+def run_profile(op_id: str, iters: int, out_dir: Path, timeout: int, warmup: int = 2) -> ProfileResult:
+    """rocprofv3 kernel trace of `warmup` + `iters` calls of the op's
+    representative target (the program itself follows `--`, with no launcher
+    in between): per-kernel statistics as CSV and the timeline as a Perfetto
+    trace, where the reference writes a torch.profiler Chrome trace."""
     rocprof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
     if not os.path.exists(rocprof):
         raise RuntimeError("rocprofv3 not found (ROCm's profiler is needed for `profile`)")
     out_dir.mkdir(parents=True, exist_ok=True)
-    cmd = [rocprof, "--kernel-trace", "--stats", "--output-format", "csv", "-d", str(out_dir), "-o", "run", "--",
-           sys.executable, "-m", "custom_cuda_kernals_amd.cli.profile_target", op_id, str(iters)]
+    cmd = [rocprof, "--kernel-trace", "--stats", "--output-format", "csv", "pftrace", "-d", str(out_dir), "-o", "run",
+           "--", sys.executable, "-m", "custom_cuda_kernals_amd.cli.profile_target", op_id, str(iters), str(warmup)]
     proc = subprocess.run(cmd, cwd=REPO_ROOT, capture_output=True, text=True, timeout=timeout)
     stats = sorted(out_dir.rglob("*kernel_stats.csv"))
     if not stats:
@@ -129,4 +132,5 @@ def run_profile(op_id: str, iters: int, out_dir: Path, timeout: int) -> ProfileR
                            f"{proc.stderr[-3000:]}")
     rows = list(csv.DictReader(open(stats[-1])))
     top = sorted(rows, key=lambda r: -float(r.get("TotalDurationNs", 0)))[:15]
-    return ProfileResult(out_dir, top)
+    traces = sorted(out_dir.rglob("*.pftrace"))
+    return ProfileResult(out_dir, top, traces[-1] if traces else None)

@@ -72,6 +72,22 @@ def test_doctor_reports_every_check():
     assert "PyTorch" in r.output
 
 
+def test_benchmark_shows_a_stored_result_without_a_gpu(tmp_path, monkeypatch):
+    """Without --rerun, `benchmark` renders the stored bench line (no GPU needed);
+    --full adds the recorded detail columns."""
+    monkeypatch.setattr(runners, "RESULTS", tmp_path)
+    line = {"ops": {"rope_inplace": {"workload": "rope_inplace_bf16_8x4096", "us": 102.1, "GB_per_s": 6593.0,
+                                     "frac_of_8TBps": 0.8242, "algorithmic_bytes": 673185792, "shape": [8, 4096],
+                                     "steps": 100, "buffer_sets": 4,
+                                     "per_call": {"median_us": 110.2, "iqr_us": 0.5, "calls": 30}}}}
+    (tmp_path / "bench_rope.json").write_text(json.dumps(line))
+    r = runner.invoke(cli_app.app, ["benchmark", "rope"])
+    assert r.exit_code == 0, r.output
+    assert "102.10" in r.output and "stored result" in r.output
+    r = runner.invoke(cli_app.app, ["benchmark", "rope", "--full"])
+    assert r.exit_code == 0 and "673185792" in r.output
+
+
 def test_visualize_from_a_stored_bench_line(tmp_path, monkeypatch):
     monkeypatch.setattr(runners, "RESULTS", tmp_path)
     monkeypatch.setattr(cli_app, "RESULTS", tmp_path)

@@ -24,10 +24,11 @@ def test_compare_kernel_beats_eager(op_id):
 
 def test_benchmark_and_profile_commands(tmp_path, monkeypatch):
     monkeypatch.setattr(runners, "RESULTS", tmp_path)
-    r = runner.invoke(cli_app.app, ["benchmark", "moe_router", "--steps", "5"])
+    r = runner.invoke(cli_app.app, ["benchmark", "moe_router", "--steps", "5", "--rerun"])
     assert r.exit_code == 0, r.output
     assert (tmp_path / "bench_moe_router.json").exists()
-    r = runner.invoke(cli_app.app, ["profile", "moe_router", "--iters", "3", "-o", str(tmp_path / "prof"),
-                                    "--timeout", "100"])
+    r = runner.invoke(cli_app.app, ["profile", "moe_router", "--warmup", "2", "--iters", "3", "-o",
+                                    str(tmp_path / "prof"), "--timeout", "100"])
     assert r.exit_code == 0, r.output
     assert "moe_router" in r.output
+    assert list((tmp_path / "prof").rglob("*.pftrace")), "no Perfetto trace written"
