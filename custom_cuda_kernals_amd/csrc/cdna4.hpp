@@ -3,8 +3,8 @@
 //   * element codecs: one 16-byte global access <-> VEC floats for fp32,
 //     fp16 and bf16 storage, with round-to-nearest-even stores
 //     (v_cvt_pk_bf16_f32 for bf16);
-//   * wave64 all-reduce through DPP (quad_perm, row_half_mirror, row_mirror)
-//     plus one ds_swizzle and two readlanes, and a one-barrier LDS stage for
+//   * wave64 all-reduce through DPP (quad_perm, row_half_mirror, row_mirror,
+//     row_bcast:15/31) and one readlane, and a one-barrier LDS stage for
 //     multi-wave workgroups;
 //   * correctly rounded division by a per-row scale at three VALU ops per
 //     element, and the PyTorch-compatible slow path for non-finite cases;

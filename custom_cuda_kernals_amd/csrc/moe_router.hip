@@ -8,7 +8,7 @@
 //
 // Design: one wave64 per token, up to 256 experts (4 per lane, expert
 // e = lane + 64 * slot). The max and the sum of the softmax are wave
-// all-reductions (DPP + ds_swizzle); each of the k selection rounds is a
+// all-reductions (DPP); each of the k selection rounds is a
 // wave arg-max in two all-reductions: the largest probability (as integer
 // bits; probabilities are >= +0) and then the smallest expert index holding
 // it. Round i's result is kept by lane i % 64, so the weights are renormalised
