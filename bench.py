@@ -143,6 +143,12 @@ def _ops(torch, native):
     ops.append(Op("fp8_quant_tensor", "fp8_tensor_bf16_2048x4096", m1 * n1 * 3 + 8, mk1g, tensor_fp8, m1 * n1 * 3,
                   [m1, n1]))
 
+    # The same op as the Python API runs it (fp8_quant(x, "e4m3", "tensor")): no
+    # amax word, so no zero-fill.
+    ops.append(Op("fp8_quant_tensor_api", "fp8_tensor_api_bf16_2048x4096", m1 * n1 * 3 + 4, mk1g,
+                  lambda b: native.fp8_quant_tensor_fwd(b["x"], b["q"], b["st"], None, "e4m3"), m1 * n1 * 3,
+                  [m1, n1]))
+
     # The same tensor granularity through the no-allocation C entry point
     # (no amax scratch, no zero-fill; library-owned partial slots).
     lib = _c_lib()

@@ -278,24 +278,52 @@ __global__ __launch_bounds__(256) void fp8_block_generic(const void* __restrict_
 // ---------------------------------------------------------------------------
 // Tensor granularity. The reference's ABI passes one caller-zeroed int32 that
 // must end up holding the amax bits (fp8_quant.cu:159-234 atomicMax-es every
-// block's maximum into it). Thousands of same-address device-scope atomics
-// serialise (26.7 us of a 33.7 us launch at [2048, 4096] bf16 on MI355X), so
-// the maximum is found in three steps instead:
-//   fp8_tensor_partial - each workgroup stores its max |x| bits into a slot of
-//                        the codes buffer (plain stores; the cast overwrites it);
-//   fp8_tensor_finish  - one workgroup reduces the slots and does the single
-//                        atomicMax into the caller's int32;
-//   fp8_tensor_cast    - the flat cast pass, which also serves static scales.
-// Max |x| is taken on non-negative fp32 bits, so integer max is float max with
-// NaN above +inf. Inputs too small to hold the slots use fp8_tensor_amax (one
-// workgroup, one atomic).
+// block's maximum into it). Same-address device-scope atomics serialise (one
+// per workgroup took 26.7 us of a 33.7 us launch at [2048, 4096] bf16 on
+// MI355X), so the maximum travels through plain stores into slots inside the
+// codes buffer, in three launches:
+//   fp8_tensor_partial - each of gp workgroups stores the max |x| bits of its
+//                        share into its slot;
+//   fp8_tensor_finish  - one workgroup reduces the slots, does the single
+//                        atomicMax into the caller's int32 and stores the scale;
+//   fp8_tensor_cast    - the flat cast pass (fp8_tensor_cast<kScaleWord>, which
+//                        reads that scale), shared with static scales.
+// Small inputs save the middle launch: the partial pass stores its maximum
+// into a slot array at the start of every cast chunk (fp8_tensor_partial
+// <REPLICATE>), each cast workgroup reduces the array in its own chunk, which
+// no other workgroup reads or writes, before overwriting the chunk with codes,
+// and cast workgroup 0 does the atomicMax and stores the scale
+// (fp8_tensor_cast<kAmaxChunk>). Inputs too small for one slot array use
+// fp8_tensor_amax (one workgroup) in the partial and finish's place.
+//
+// The caller's int32 may be null (an addition: the Python API has no use for
+// it). Otherwise it ends up holding max(its initial value, amax bits) and the
+// scale follows from that maximum, as in the reference. Max |x| is taken on
+// non-negative fp32 bits, so integer max is float max with NaN above +inf.
 // ---------------------------------------------------------------------------
 constexpr int kPartialThreads = 512, kPartialUnroll = 4, kPartialMaxGroups = 512;
 
-// Each workgroup stores its max |x| bits into partial[blockIdx.x].
-template <class C, bool VECTOR>
+// Where the cast takes the dynamic scale from.
+enum AmaxSource : int {
+  kScaleWord = 0,  // scale_out[0], stored by fp8_tensor_finish / fp8_tensor_amax
+  kAmaxSlots = 1,  // `nslots` partial maxima at `slots` (the no-allocation entry point's scratch)
+  kAmaxChunk = 2,  // `nslots` partial maxima at the start of the workgroup's own chunk of codes
+};
+
+// Slot of partial workgroup p in a slot array: the slots of one XCD's
+// workgroups (p % 8; workgroups are dealt to the XCDs round-robin) are
+// contiguous, so each cache line of a replicated array is written from one L2.
+__device__ inline int partial_slot(int p, int groups) {
+  return groups % 8 == 0 ? (p % 8) * (groups / 8) + p / 8 : p;
+}
+
+// Each workgroup's max |x| bits go to partial[blockIdx.x] or, with REPLICATE,
+// to its slot of each of the `chunks` slot arrays at q + c * chunk_bytes.
+template <class C, bool VECTOR, bool REPLICATE = false>
 __global__ __launch_bounds__(kPartialThreads) void fp8_tensor_partial(const void* __restrict__ x, int64_t total,
-                                                                      uint32_t* __restrict__ partial) {
+                                                                      uint32_t* __restrict__ partial,
+                                                                      uint8_t* __restrict__ q = nullptr,
+                                                                      int64_t chunk_bytes = 0, int chunks = 0) {
   constexpr int T = kPartialThreads, U = kPartialUnroll;
   __shared__ uint32_t lds[2 * (T / 64)];
   uint32_t acc = 0;
@@ -323,22 +351,46 @@ __global__ __launch_bounds__(kPartialThreads) void fp8_tensor_partial(const void
     acc = C::absmax1(x, i, acc);
   }
   acc = block_allreduce<T / 64>(acc, typename AmaxOp<C>::type{}, lds, 0);
-  if (threadIdx.x == 0) partial[blockIdx.x] = f32_bits(C::absmax_to_float(acc));
+  const uint32_t bits = f32_bits(C::absmax_to_float(acc));
+  if constexpr (REPLICATE) {
+    const int64_t off = 4 * (int64_t)partial_slot((int)blockIdx.x, (int)gridDim.x);
+    for (int c = threadIdx.x; c < chunks; c += T) *reinterpret_cast<uint32_t*>(q + c * chunk_bytes + off) = bits;
+  } else {
+    if (threadIdx.x == 0) partial[blockIdx.x] = bits;
+  }
 }
 
+// The tensor's amax into the caller's int32 (if any; `initial` is its value
+// before the op) and the scale of max(initial, amax) into scale_out[0]. The
+// atomicMax's result is not waited for.
+template <int FMT>
+__device__ inline void publish_amax(uint32_t amax_bits, int32_t initial, int32_t* amax_scratch, float* scale_out) {
+  if (amax_scratch != nullptr) {
+    atomicMax(amax_scratch, (int32_t)amax_bits);
+    amax_bits = (uint32_t)max(initial, (int32_t)amax_bits);
+  }
+  scale_out[0] = scale_from_amax<FMT>(bits_f32(amax_bits));
+}
+
+template <int FMT>
 __global__ __launch_bounds__(256) void fp8_tensor_finish(const uint32_t* __restrict__ partial, int n_partial,
-                                                         int32_t* __restrict__ amax_bits) {
+                                                         int32_t* __restrict__ amax_scratch,
+                                                         float* __restrict__ scale_out) {
   __shared__ uint32_t lds[2 * 4];
+  // Only this launch writes the caller's int32, so its value now is the initial one.
+  const int32_t initial = (amax_scratch != nullptr && threadIdx.x == 0) ? *amax_scratch : 0;
   uint32_t acc = 0;
   for (int i = threadIdx.x; i < n_partial; i += 256) acc = max(acc, partial[i]);
   acc = block_allreduce<4>(acc, MaxU32{}, lds, 0);
-  if (threadIdx.x == 0) atomicMax(amax_bits, (int32_t)acc);
+  if (threadIdx.x == 0) publish_amax<FMT>(acc, initial, amax_scratch, scale_out);
 }
 
-template <class C, bool VECTOR>
+template <class C, int FMT, bool VECTOR>
 __global__ __launch_bounds__(256) void fp8_tensor_amax(const void* __restrict__ x, int64_t total,
-                                                       int32_t* __restrict__ amax_bits) {
+                                                       int32_t* __restrict__ amax_scratch,
+                                                       float* __restrict__ scale_out) {
   __shared__ uint32_t lds[2 * 4];
+  const int32_t initial = (amax_scratch != nullptr && threadIdx.x == 0) ? *amax_scratch : 0;
   uint32_t acc = 0;
   const int64_t stride = (int64_t)gridDim.x * 256;
   const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -351,28 +403,39 @@ __global__ __launch_bounds__(256) void fp8_tensor_amax(const void* __restrict__ 
     for (int64_t i = tid; i < total; i += stride) acc = C::absmax1(x, i, acc);
   }
   acc = block_allreduce<4>(acc, typename AmaxOp<C>::type{}, lds, 0);
-  if (threadIdx.x == 0) atomicMax(amax_bits, (int32_t)f32_bits(C::absmax_to_float(acc)));
+  if (threadIdx.x == 0) publish_amax<FMT>(f32_bits(C::absmax_to_float(acc)), initial, amax_scratch, scale_out);
 }
 
-// STATIC: scale is `static_scale`; otherwise it derives from *amax_bits and is
-// written to scale_out[0]. VECTOR: CAST_THREADS threads with CAST_UNROLL
-// 16-byte vectors each, loaded before any is converted; measured on MI355X
-// against 256 threads with one vector per grid-stride step and cached code
-// stores: 32.3 vs 35.7 us at [16384, 4096] bf16, 248 vs 338 us at [65536, 8192].
+// STATIC: scale is `static_scale`; otherwise it comes from SRC. VECTOR:
+// CAST_THREADS threads with CAST_UNROLL 16-byte vectors each, loaded before
+// any is converted; measured on MI355X against 256 threads with one vector per
+// grid-stride step and cached code stores: 32.3 vs 35.7 us at [16384, 4096]
+// bf16, 248 vs 338 us at [65536, 8192].
 constexpr int kCastThreads = 512, kCastUnroll = 2;
 static_assert(kPartialThreads * kPartialUnroll == 2 * kCastThreads * kCastUnroll,
               "the XCD-aligned cast order takes halves of the partial pass's chunks");
 
-// SLOTS: the dynamic scale comes from the `nslots` partial maxima in `slots`
-// (each workgroup reduces them itself; the first vectors' loads are issued
-// before that reduction), not from *amax_bits.
-template <class C, int FMT, bool STATIC, bool VECTOR, bool SLOTS = false>
+// Codes bytes of one vector-path cast chunk (the first chunk of workgroup b
+// starts at b times this).
+template <class C>
+constexpr int64_t kCastChunkBytes = (int64_t)kCastThreads * kCastUnroll * C::VEC;
+
+// Replicated slot arrays cost gp x g scattered 4-byte stores (gp partial
+// workgroups, g cast chunks), each its own cache-line write at the L2, against
+// the one launch they save. Measured per op on MI355X (bf16, graph-replayed,
+// with the caller's zero-fill): [512, 4096] 8.7 vs 9.4 us (32 K stores),
+// [1024, 4096] 10.0 vs 10.6 us (128 K), [2048, 4096] 13.7 vs 12.5 us (512 K),
+// [4096, 4096] 24.2 vs 19.1 us (1 M).
+constexpr int64_t kMaxReplicatedSlots = 1 << 17;
+
+template <class C, int FMT, bool STATIC, bool VECTOR, int SRC = kScaleWord>
 __global__ __launch_bounds__(VECTOR ? kCastThreads : 256) void fp8_tensor_cast(
     const void* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ scale_out,
-    const int32_t* __restrict__ amax_bits, float static_scale, int64_t total, bool xcd_aligned = false,
+    int32_t* __restrict__ amax_scratch, float static_scale, int64_t total, bool xcd_aligned = false,
     const uint32_t* __restrict__ slots = nullptr, int nslots = 0) {
   constexpr int T = VECTOR ? kCastThreads : 256;
   constexpr int U = VECTOR ? kCastUnroll : 1;
+  static_assert(VECTOR || SRC != kAmaxChunk, "chunk slot arrays belong to the vector path");
   const int64_t nvec = VECTOR ? total / C::VEC : 0;
   const u32x4* xv = static_cast<const u32x4*>(x);
   int64_t bid = blockIdx.x;
@@ -402,23 +465,33 @@ __global__ __launch_bounds__(VECTOR ? kCastThreads : 256) void fp8_tensor_cast(
     }
   };
   if constexpr (VECTOR) load(b);
-  float s, amax_t = 0.0f;
+  float s;
   if constexpr (STATIC) {
     s = static_scale;
+  } else if constexpr (SRC == kScaleWord) {
+    s = scale_out[0];
   } else {
-    if constexpr (SLOTS) {
-      __shared__ uint32_t lds[2 * (T / 64)];
-      uint32_t m = 0;
-      for (int i = threadIdx.x; i < nslots; i += T) m = max(m, slots[i]);
-      amax_t = bits_f32(block_allreduce<T / 64>(m, MaxU32{}, lds, 0));
-    } else {
-      amax_t = bits_f32((uint32_t)*amax_bits);
+    // The maximum of the slots (loaded after this workgroup's first vectors),
+    // and for chunk slot arrays the caller's int32, read before workgroup 0's
+    // atomicMax (its initial value) or after it (the same overall maximum).
+    __shared__ uint32_t lds[2 * (T / 64)];
+    const uint32_t* sl = slots;
+    if constexpr (SRC == kAmaxChunk) sl = reinterpret_cast<const uint32_t*>(q + bid * kCastChunkBytes<C>);
+    const bool word = SRC == kAmaxChunk && amax_scratch != nullptr;
+    const int32_t seen = word ? __hip_atomic_load(amax_scratch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < nslots; i += T) m = max(m, sl[i]);
+    m = block_allreduce<T / 64>(m, MaxU32{}, lds, 0);
+    s = scale_from_amax<FMT>(bits_f32(word ? (uint32_t)max(seen, (int32_t)m) : m));
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      if (word) atomicMax(amax_scratch, (int32_t)m);
+      scale_out[0] = s;
     }
-    s = scale_from_amax<FMT>(amax_t);
-    if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
   }
   const float r = 1.0f / s;
-  const bool fast_t = fast_path_ok<FMT>(s, r, amax_t);
+  // A dynamic scale s = amax / FP8_MAX (or the clamp) keeps |x| * (1/s) within
+  // the conversion's verified range, so only s and 1/s need checking.
+  const bool fast_t = fast_path_ok<FMT>(s, r, 0.0f);
   int64_t done = 0;
   if constexpr (VECTOR) {
     const int64_t stride = (int64_t)gridDim.x * T * U;
@@ -755,9 +828,22 @@ extern "C" int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, fl
     return with_fp8(fp8_format, [&](auto f) {
       constexpr int FMT = decltype(f)::value;
       const bool vec_ok = host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
-      // Partial-max slots: 4-byte words inside the codes buffer.
-      const unsigned gp = vec_ok ? flat_grid(total / C::VEC, kPartialThreads * kPartialUnroll, kPartialMaxGroups)
+      const int64_t nvec = total / C::VEC;
+      const unsigned gp = vec_ok ? flat_grid(nvec, kPartialThreads * kPartialUnroll, kPartialMaxGroups)
                                  : flat_grid(total, kPartialThreads * 16, kPartialMaxGroups);
+      if (vec_ok) {
+        bool aligned = false;
+        const unsigned g = tensor_cast_grid(nvec, gp, &aligned);
+        // Every cast chunk, the last one included, holds a slot array.
+        const int64_t cb = kCastChunkBytes<C>;
+        if ((int64_t)gp * g <= kMaxReplicatedSlots && nvec * C::VEC - (int64_t)(g - 1) * cb >= 4 * (int64_t)gp) {
+          fp8_tensor_partial<C, true, true><<<gp, kPartialThreads, 0, st>>>(x, total, nullptr, x_fp8, cb, (int)g);
+          fp8_tensor_cast<C, FMT, false, true, kAmaxChunk><<<g, kCastThreads, 0, st>>>(
+              x, x_fp8, scale, amax_scratch, 0.0f, total, aligned, nullptr, (int)gp);
+          return launch_status();
+        }
+      }
+      // One slot array: 4-byte words at the first aligned word of the codes buffer.
       const uintptr_t slots = (reinterpret_cast<uintptr_t>(x_fp8) + 3) & ~uintptr_t(3);
       uint32_t* partial = reinterpret_cast<uint32_t*>(slots);
       const bool slots_fit = (int64_t)(slots - reinterpret_cast<uintptr_t>(x_fp8)) + 4 * (int64_t)gp <= total;
@@ -767,20 +853,20 @@ extern "C" int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, fl
         } else {
           fp8_tensor_partial<C, false><<<gp, kPartialThreads, 0, st>>>(x, total, partial);
         }
-        fp8_tensor_finish<<<1, 256, 0, st>>>(partial, (int)gp, amax_scratch);
+        fp8_tensor_finish<FMT><<<1, 256, 0, st>>>(partial, (int)gp, amax_scratch, scale);
       } else if (vec_ok) {
-        fp8_tensor_amax<C, true><<<1, 256, 0, st>>>(x, total, amax_scratch);
+        fp8_tensor_amax<C, FMT, true><<<1, 256, 0, st>>>(x, total, amax_scratch, scale);
       } else {
-        fp8_tensor_amax<C, false><<<1, 256, 0, st>>>(x, total, amax_scratch);
+        fp8_tensor_amax<C, FMT, false><<<1, 256, 0, st>>>(x, total, amax_scratch, scale);
       }
       if (vec_ok) {
         bool aligned = false;
-        const unsigned g = tensor_cast_grid(total / C::VEC, slots_fit ? gp : 0u, &aligned);
-        fp8_tensor_cast<C, FMT, false, true><<<g, kCastThreads, 0, st>>>(x, x_fp8, scale, amax_scratch, 0.0f,
-                                                                          total, aligned);
+        const unsigned g = tensor_cast_grid(nvec, slots_fit ? gp : 0u, &aligned);
+        fp8_tensor_cast<C, FMT, false, true><<<g, kCastThreads, 0, st>>>(x, x_fp8, scale, nullptr, 0.0f, total,
+                                                                          aligned);
       } else {
-        const unsigned g = flat_grid(total / C::VEC, 256, 2048);
-        fp8_tensor_cast<C, FMT, false, false><<<g, 256, 0, st>>>(x, x_fp8, scale, amax_scratch, 0.0f, total);
+        const unsigned g = flat_grid(nvec, 256, 2048);
+        fp8_tensor_cast<C, FMT, false, false><<<g, 256, 0, st>>>(x, x_fp8, scale, nullptr, 0.0f, total);
       }
       return launch_status();
     });
@@ -833,13 +919,13 @@ extern "C" int32_t launch_fp8_quant_tensor_noalloc_fwd(const void* x, uint8_t* x
         fp8_tensor_partial<C, true><<<gp, kPartialThreads, 0, st>>>(x, total, scr);
         bool aligned = false;
         const unsigned g = tensor_cast_grid(total / C::VEC, gp, &aligned);
-        fp8_tensor_cast<C, FMT, false, true, true><<<g, kCastThreads, 0, st>>>(x, x_fp8, scale, nullptr, 0.0f, total,
+        fp8_tensor_cast<C, FMT, false, true, kAmaxSlots><<<g, kCastThreads, 0, st>>>(x, x_fp8, scale, nullptr, 0.0f, total,
                                                                                 aligned, scr, (int)gp);
       } else {
         const unsigned gp = flat_grid(total, kPartialThreads * 16, kPartialMaxGroups);
         fp8_tensor_partial<C, false><<<gp, kPartialThreads, 0, st>>>(x, total, scr);
         const unsigned g = flat_grid(total / C::VEC, 256, 2048);
-        fp8_tensor_cast<C, FMT, false, false, true><<<g, 256, 0, st>>>(x, x_fp8, scale, nullptr, 0.0f, total, false,
+        fp8_tensor_cast<C, FMT, false, false, kAmaxSlots><<<g, 256, 0, st>>>(x, x_fp8, scale, nullptr, 0.0f, total, false,
                                                                         scr, (int)gp);
       }
       return launch_status();

@@ -346,18 +346,21 @@ void fp8_quant_tensor_fwd(py::handle x, py::handle x_fp8, py::handle scale, py::
   View xv = validate_tensor("x", x);
   View qv = validate_tensor("x_fp8", x_fp8);
   View sv = validate_tensor("scale", scale);
-  View av = validate_int32_tensor("amax_scratch", amax_scratch);
+  // None (an addition) skips the caller-visible amax word; the Python API
+  // passes it, having no use for that word.
+  std::optional<View> av;
+  if (!amax_scratch.is_none()) av = validate_int32_tensor("amax_scratch", amax_scratch);
   check_fp8_common(xv, qv, fmt, fmt_str);
   require_f32("scale", sv);
   check_2d_and_codes(xv, qv);
-  if (product(av.shape, 0, av.shape.size()) != 1) {
-    shape_mismatch("amax_scratch must have exactly 1 element; got shape " + shape_str(av.shape));
+  if (av && product(av->shape, 0, av->shape.size()) != 1) {
+    shape_mismatch("amax_scratch must have exactly 1 element; got shape " + shape_str(av->shape));
   }
   const int64_t m = xv.shape[0], n = xv.shape[1];
   void* st = current_stream(xv.device_index);
   check_launch("launch_fp8_quant_tensor_fwd",
                launch_fp8_quant_tensor_fwd((const void*)xv.ptr, (uint8_t*)qv.ptr, (float*)sv.ptr,
-                                           (int32_t*)av.ptr, m, n, xv.dtype, fmt, st));
+                                           av ? (int32_t*)av->ptr : nullptr, m, n, xv.dtype, fmt, st));
 }
 
 // ---- additive functions ----------------------------------------------------

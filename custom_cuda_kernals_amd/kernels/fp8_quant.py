@@ -69,7 +69,9 @@ def fp8_quant(
         native.fp8_quant_token_fwd(x, x_fp8, scales, fp8_format)
         return x_fp8, scales
 
+    # The reference zero-fills an int32 that receives the amax bits and then
+    # drops it; None skips that word (and the fill launch) with the same codes
+    # and scale.
     scales = torch.empty(1, dtype=torch.float32, device=device)
-    amax_scratch = torch.zeros(1, dtype=torch.int32, device=device)
-    native.fp8_quant_tensor_fwd(x, x_fp8, scales, amax_scratch, fp8_format)
+    native.fp8_quant_tensor_fwd(x, x_fp8, scales, None, fp8_format)
     return x_fp8, scales

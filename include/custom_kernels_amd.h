@@ -72,8 +72,10 @@ int32_t launch_fp8_quant_block_fwd(const void* x, uint8_t* x_fp8, float* scale, 
 
 /* Dynamic FP8, one scale for the matrix; scale: float32 [1]; amax_scratch:
  * int32 [1], caller-zeroed before every call, left holding the bits of
- * max |x| (atomically max-ed in, as in the reference). Between the call's
- * kernels, x_fp8 also holds per-workgroup maxima, which the cast overwrites.
+ * max |x| (atomically max-ed in, as in the reference; a nonzero initial value
+ * takes part in the maximum and so in the scale). amax_scratch may be NULL
+ * (an addition): then no amax word is written. Between the call's kernels,
+ * x_fp8 also holds per-workgroup maxima, which the cast overwrites.
  * Replaces reference csrc/includes/fp8_quant.h:51-60. */
 int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, float* scale,
                                     int32_t* amax_scratch, int64_t m, int64_t n, int32_t dtype,

@@ -158,18 +158,66 @@ def test_tensor_amax_found_anywhere(shape, where):
     _check(x, "e4m3", "tensor")
 
 
-def _tensor_abi(x_dev: torch.Tensor, q: torch.Tensor, scratch: torch.Tensor, fmt_tag: int = 3):
+def _tensor_abi(x_dev: torch.Tensor, q: torch.Tensor, scratch: torch.Tensor | None, fmt_tag: int = 3):
     from tests import _cck
 
     lib = _cck.load()
     scale = torch.empty(1, dtype=torch.float32, device="cuda")
     m, n = x_dev.shape
     dtag = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[x_dev.dtype]
-    rc = lib.launch_fp8_quant_tensor_fwd(x_dev.data_ptr(), q.data_ptr(), scale.data_ptr(), scratch.data_ptr(), m, n,
+    rc = lib.launch_fp8_quant_tensor_fwd(x_dev.data_ptr(), q.data_ptr(), scale.data_ptr(),
+                                         None if scratch is None else scratch.data_ptr(), m, n,
                                          dtag, fmt_tag, torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     torch.cuda.synchronize()
     return scale
+
+
+# (shape, what it reaches for bf16 / fp16; fp32 alike unless noted)
+TENSOR_PATHS = [
+    ((1024, 4096), "bf16/fp16: slot arrays in every cast chunk, XCD-aligned cast order; fp32: the finishing launch"),
+    ((300, 4096), "slot arrays written by 75 partial workgroups (not a multiple of 8), chunks walked last-first"),
+    ((2048, 4096), "the finishing launch, XCD-aligned cast order (config 1)"),
+    ((4099, 4097), "the finishing launch, a scalar tail after the vectors"),
+    ((4, 20482), "last cast chunk too short for a slot array: the finishing launch"),
+    ((5, 2056), "slot arrays: one or two partial workgroups, two or three cast chunks"),
+    ((2, 3), "bf16/fp16: no whole vector, the finishing launch over scalars; fp32: a one-word slot array, a tail"),
+    ((1, 8), "one vector: a slot array in the only chunk"),
+    ((1, 3), "too small for one slot: the one-workgroup amax"),
+]
+
+
+@pytest.mark.parametrize("scratch", ["zeroed", "preset", "none"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("shape", [s for s, _ in TENSOR_PATHS], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_tensor_paths_through_the_abi(shape, dtype, scratch):
+    """Each of the launcher's paths, with the caller's int32 zeroed (the
+    reference's contract), preset above the tensor's amax (which then sets the
+    scale) and absent (NULL): codes and scale bit-exact, the int32 left at
+    max(initial, amax bits), and nothing written outside the codes buffer."""
+    x = inputs.randn(shape, dtype, seed=shape[0] * 7 + shape[1])
+    x.view(-1)[x.numel() // 3] = 30.0
+    x32 = x.float().numpy()
+    amax = np.float32(np.abs(x32).max())
+    m, n = shape
+    buf = torch.full((m * n + 512,), 0x55, dtype=torch.uint8, device="cuda")
+    q = buf[256:256 + m * n].view(m, n)
+    init = {"zeroed": 0, "preset": int(np.array([1000.0], dtype=np.float32).view(np.int32)[0]), "none": None}[scratch]
+    word = None if init is None else torch.tensor([init], dtype=torch.int32, device="cuda")
+    scale = _tensor_abi(x.cuda(), q, word)
+    if scratch == "preset":
+        s_ref = np.float32(np.float32(1000.0) / np.float32(448.0))
+        assert_f32_bits_equal(scale, np.array([s_ref], dtype=np.float32))
+        assert_codes_equal(q, ofp8.quant_static(x32, float(s_ref), "e4m3"))
+    else:
+        codes, s_ref = ofp8.quant_tensor(x32, "e4m3")
+        assert_codes_equal(q, codes)
+        assert_f32_bits_equal(scale, s_ref)
+    if word is not None:
+        want = max(init, int(np.array([amax], dtype=np.float32).view(np.int32)[0]))
+        assert int(word.item()) == want
+    b = buf.cpu().numpy()
+    assert (b[:256] == 0x55).all() and (b[256 + m * n:] == 0x55).all(), "wrote outside the codes buffer"
 
 
 @pytest.mark.parametrize("offset", [1, 2, 3])
