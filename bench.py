@@ -265,6 +265,16 @@ def _ops(torch, native):
 
     ops.append(Op("moe_router", "moe_router_f32_2048x160_top6", rt * re_ * 4 + rt * rk * 12, mkr,
                   lambda b: native.moe_router_fwd(b["lg"], b["w"], b["i"], True), rt * re_ * 4, [rt, re_, rk]))
+
+    # The index bookkeeping between them (compute_permutation with num_experts):
+    # the router's [2048, 6] expert ids in, permute / unpermute int64 out.
+    def mkp():
+        return dict(ids=torch.randint(0, re_, (rt, rk), device=dev, generator=g),
+                    p=torch.empty(rt * rk, dtype=torch.int64, device=dev),
+                    u=torch.empty(rt, rk, dtype=torch.int64, device=dev))
+
+    ops.append(Op("moe_permutation", "moe_permutation_2048x6_of_160", rt * rk * 24, mkp,
+                  lambda b: native.moe_permutation_fwd(b["ids"], b["p"], b["u"], re_), rt * rk * 24, [rt, rk, re_]))
     return ops
 
 
@@ -391,6 +401,21 @@ def _anchors(torch, steps, warmup):
         r = _time_op(torch, op, steps, warmup, per_call=False)
         out[name] = {"bounds": "fp8_quant_token", "us": r["us"], "GB_per_s": r["GB_per_s"],
                      "frac_of_8TBps": r["frac_of_8TBps"], "bytes": nbytes}
+
+    # The reference's own bookkeeping (baselines/token_permute.py:55-70: a
+    # stable torch.argsort and its inverse) on the same [2048, 6] ids.
+    from custom_cuda_kernals_amd.kernels import compute_permutation
+
+    t, k, e = 2048, 6, 160
+
+    def make_ids():
+        return {"ids": torch.randint(0, e, (t, k), device="cuda")}
+
+    op = Op("torch_compute_permutation", "moe_permutation_2048x6_of_160", t * k * 24, make_ids,
+            lambda b: compute_permutation(b["ids"]), t * k * 24, [t, k, e])
+    r = _time_op(torch, op, steps, warmup, per_call=False)
+    out["torch_compute_permutation"] = {"bounds": "moe_permutation", "us": r["us"], "GB_per_s": r["GB_per_s"],
+                                        "frac_of_8TBps": r["frac_of_8TBps"], "bytes": t * k * 24}
     return out
 
 

@@ -269,8 +269,8 @@ REGISTRY: dict[str, OpSpec] = {
                             "launch_fp8_quant_static_fwd"),
             sources=(_CSRC + "fp8_quant.hip", _CSRC + "fp8_codec.hpp", _CSRC + "cdna4.hpp"),
             test_files=("tests/test_fp8_quant_gpu.py", "tests/test_oracle_fp8.py", "tests/test_zz_no_alloc.py"),
-            bench_ops=("fp8_quant_token", "fp8_quant_block", "fp8_quant_tensor", "fp8_quant_tensor_noalloc",
-                       "fp8_quant_static"),
+            bench_ops=("fp8_quant_token", "fp8_quant_block", "fp8_quant_tensor", "fp8_quant_tensor_api",
+                       "fp8_quant_tensor_noalloc", "fp8_quant_static"),
             build_target=_t_fp8),
         OpSpec(
             id="rmsnorm_residual_fp8", number=5, title="Fused residual add + RMSNorm + FP8 quantisation",
@@ -303,16 +303,20 @@ REGISTRY: dict[str, OpSpec] = {
             formula="dst[i] = src[idx[i]]; out[t] = sum_j w[t, j] * eo[ui[t, j]] (fp32, j order)",
             dtypes=("float32", "float16", "bfloat16", "fp8 (gather)"),
             memory_profile="HBM-bound row moves (gather 67 MB, combine k = 2 50 MB at the reference's shapes).",
-            design=("four destination rows per gather workgroup", "two expert rows in flight per combine step"),
-            target="gather bit-exact; combine equal to the j-order fp32 sum",
+            design=("four destination rows per gather workgroup", "two expert rows in flight per combine step",
+                    "the permutation bookkeeping as one stable counting-sort launch (compute_permutation with "
+                    "num_experts)"),
+            target="gather and the permutation bit-exact; combine equal to the j-order fp32 sum",
             reference=("baselines/token_permute.py:55-70, 215-251", "csrc/kernels/token_permute.cu",
                        "csrc/includes/token_permute.h:17-41"),
             python_api=("token_gather", "token_combine", "compute_permutation"),
             c_entry_points=("launch_token_gather_fwd", "launch_token_combine_fwd",
-                            "launch_token_gather_checked_fwd", "launch_token_combine_checked_fwd"),
+                            "launch_token_gather_checked_fwd", "launch_token_combine_checked_fwd",
+                            "launch_moe_permutation_fwd"),
             sources=(_CSRC + "token_permute.hip",), test_files=("tests/test_token_permute_gpu.py",
                                                                  "tests/test_oracle_moe.py"),
-            bench_ops=("token_gather", "token_combine_k2", "token_combine_k6"), build_target=_t_token_permute),
+            bench_ops=("token_gather", "token_combine_k2", "token_combine_k6", "moe_permutation"),
+            build_target=_t_token_permute),
         OpSpec(
             id="moe_router", number=8, title="Softmax top-k MoE router",
             purpose="Per token: softmax over expert logits, the k largest probabilities, renormalised.",

@@ -540,6 +540,32 @@ void token_combine_fwd(py::handle expert_output, py::handle unpermute_index, py:
 }
 
 // src/kernels/moe_router.rs:36-116.
+// Additive (baselines/token_permute.py:55-70 as one kernel).
+void moe_permutation_fwd(py::handle topk_indices, py::handle permute_index, py::handle unpermute_index,
+                         int64_t num_experts) {
+  View tv = validate_int64_tensor("topk_indices", topk_indices);
+  View pv = validate_int64_tensor("permute_index", permute_index);
+  View uv = validate_int64_tensor("unpermute_index", unpermute_index);
+  if (tv.shape.size() != 2) {
+    shape_mismatch("topk_indices must be 2-D [num_tokens, k], got " + shape_str(tv.shape));
+  }
+  const int64_t n_tokens = tv.shape[0], k = tv.shape[1];
+  if (pv.shape != std::vector<int64_t>{n_tokens * k}) {
+    shape_mismatch("permute_index shape " + shape_str(pv.shape) + " must be [" + std::to_string(n_tokens * k) + "]");
+  }
+  if (uv.shape != tv.shape) {
+    shape_mismatch("unpermute_index shape " + shape_str(uv.shape) + " must match topk_indices' " +
+                   shape_str(tv.shape));
+  }
+  if (num_experts < 1 || num_experts > 256) {
+    shape_mismatch("num_experts (" + std::to_string(num_experts) + ") must be in [1, 256]");
+  }
+  void* st = current_stream(tv.device_index);
+  check_launch("launch_moe_permutation_fwd",
+               launch_moe_permutation_fwd((const int64_t*)tv.ptr, (int64_t*)pv.ptr, (int64_t*)uv.ptr, n_tokens, k,
+                                          num_experts, st));
+}
+
 void moe_router_fwd(py::handle logits, py::handle topk_weights, py::handle topk_indices, bool renormalize) {
   View lv = validate_tensor("logits", logits);
   View wv = validate_tensor("topk_weights", topk_weights);
@@ -594,6 +620,8 @@ PYBIND11_MODULE(_native, m) {
   m.def("token_gather_fwd", &token_gather_fwd, py::arg("src"), py::arg("indices"), py::arg("dst"));
   m.def("token_combine_fwd", &token_combine_fwd, py::arg("expert_output"), py::arg("unpermute_index"),
         py::arg("weights"), py::arg("combined"));
+  m.def("moe_permutation_fwd", &moe_permutation_fwd, py::arg("topk_indices"), py::arg("permute_index"),
+        py::arg("unpermute_index"), py::arg("num_experts"));
   m.def("moe_router_fwd", &moe_router_fwd, py::arg("logits"), py::arg("topk_weights"), py::arg("topk_indices"),
         py::arg("renormalize"));
   m.def("swiglu_fp8_fwd", &swiglu_fp8_fwd, py::arg("gate"), py::arg("up"), py::arg("y_fp8"), py::arg("scale"),

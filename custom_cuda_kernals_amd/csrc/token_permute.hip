@@ -267,6 +267,127 @@ int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, 
 
 constexpr int64_t kNoBound = INT64_MAX;
 
+// ---------------------------------------------------------------------------
+// The permutation bookkeeping between the router and the gather
+// (baselines/token_permute.py:55-70, there a stable torch.argsort of the
+// flattened [T, k] expert ids and its inverse):
+//   permute_index[p]   = i / k for the i-th entry in (expert, i) order
+//   unpermute_index[i] = p, its position in that order.
+// Expert ids are bounded, so this is a stable counting sort in one launch.
+// Entries whose id lies outside [0, n_experts) go to one extra bucket after
+// every expert (so the outputs stay a permutation of [0, n)).
+//
+// G workgroups (at most kPermMaxGroups), workgroup c owning entries
+// [c * chunk, (c + 1) * chunk) in tiles of kPermThreads:
+//   1. every workgroup counts all n ids per bucket in LDS, those before its
+//      chunk (before) and the others (after), one LDS atomic per id:
+//      base[b] = (ids in buckets below b) + before[b];
+//   2. per tile, every lane ORs its lane bit into its wave's mask of its
+//      bucket (LDS); the bits below a lane in its own mask rank it among the
+//      wave's lanes of the same bucket, the popcounts of the lower waves'
+//      masks offset it, so ties keep index order; a running count per bucket
+//      carries the order from tile to tile.
+// Each workgroup reads all n ids once more than a per-chunk count would, so
+// the grid is capped: at n = 12288 (2048 tokens, top 6) that is 12 workgroups
+// and 1.2 MB of L2 reads.
+// ---------------------------------------------------------------------------
+constexpr int kPermThreads = 1024, kPermWaves = kPermThreads / 64;
+constexpr int kPermMaxExperts = 256, kPermBuckets = kPermMaxExperts + 1;
+constexpr int kPermMaxGroups = 64, kPermUnroll = 16;
+constexpr int kPermPerLane = (kPermBuckets + 63) / 64;
+
+__device__ inline uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__global__ __launch_bounds__(kPermThreads) void moe_permutation(const int64_t* __restrict__ ids, int64_t n, int64_t k,
+                                                                int n_experts, int64_t chunk,
+                                                                int64_t* __restrict__ permute_index,
+                                                                int64_t* __restrict__ unpermute_index) {
+  __shared__ uint32_t after[kPermBuckets], before[kPermBuckets], base[kPermBuckets];
+  __shared__ unsigned long long lane_mask[kPermWaves][kPermBuckets];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb = n_experts + 1;
+  auto bucket = [&](int64_t id) { return (id >= 0 && id < n_experts) ? (int)id : n_experts; };
+  for (int i = tid; i < nb; i += kPermThreads) {
+    after[i] = 0u;
+    before[i] = 0u;
+  }
+  for (int i = tid; i < kPermWaves * kPermBuckets; i += kPermThreads) (&lane_mask[0][0])[i] = 0ull;
+  __syncthreads();
+  const int64_t c0 = (int64_t)blockIdx.x * chunk;
+  const int64_t c1 = c0 + chunk < n ? c0 + chunk : n;
+  // kPermUnroll ids per thread in flight before their LDS atomics (one DRAM
+  // round trip per kPermUnroll ids instead of per id).
+  for (int64_t j0 = tid; j0 < n; j0 += (int64_t)kPermThreads * kPermUnroll) {
+    int64_t v[kPermUnroll];
+#pragma unroll
+    for (int u = 0; u < kPermUnroll; ++u) {
+      const int64_t j = j0 + (int64_t)u * kPermThreads;
+      v[u] = j < n ? ids[j] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kPermUnroll; ++u) {
+      const int64_t j = j0 + (int64_t)u * kPermThreads;
+      if (j < n) {
+        atomicAdd(j < c0 ? &before[bucket(v[u])] : &after[bucket(v[u])], 1u);
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // Exclusive scan of the bucket totals: lane l holds buckets
+    // [l * kPermPerLane, (l + 1) * kPermPerLane).
+    uint32_t loc[kPermPerLane], sum = 0u;
+#pragma unroll
+    for (int i = 0; i < kPermPerLane; ++i) {
+      const int b = lane * kPermPerLane + i;
+      loc[i] = b < nb ? before[b] + after[b] : 0u;
+      sum += loc[i];
+    }
+    uint32_t incl = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t o = __shfl_up(incl, d);
+      if (lane >= d) incl += o;
+    }
+    uint32_t run = incl - sum;
+#pragma unroll
+    for (int i = 0; i < kPermPerLane; ++i) {
+      const int b = lane * kPermPerLane + i;
+      if (b < nb) base[b] = run + before[b];
+      run += loc[i];
+    }
+  }
+  __syncthreads();
+  for (int64_t t0 = c0; t0 < c1; t0 += kPermThreads) {
+    const int64_t j = t0 + tid;
+    const bool valid = j < c1;
+    const int b = valid ? bucket(ids[j]) : 0;
+    if (valid) atomicOr(&lane_mask[wave][b], 1ull << lane);
+    __syncthreads();
+    if (valid) {
+      uint32_t pos = base[b] + lanes_below(lane_mask[wave][b]);
+      for (int w = 0; w < wave; ++w) pos += (uint32_t)__popcll(lane_mask[w][b]);
+      permute_index[pos] = j / k;
+      unpermute_index[j] = pos;
+    }
+    __syncthreads();
+    // Carry this tile's counts into base and clear the masks for the next tile.
+    for (int i = tid; i < nb; i += kPermThreads) {
+      uint32_t c = 0u;
+#pragma unroll
+      for (int w = 0; w < kPermWaves; ++w) {
+        c += (uint32_t)__popcll(lane_mask[w][i]);
+        lane_mask[w][i] = 0ull;
+      }
+      base[i] += c;
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace
 }  // namespace cck
 
@@ -299,4 +420,20 @@ extern "C" int32_t launch_token_combine_checked_fwd(const void* expert_output, c
   if (n_expert_rows < 0) return (int32_t)hipErrorInvalidValue;
   return combine(expert_output, unpermute_index, weights, combined, n_tokens, k, hidden_dim, dtype,
                  n_expert_rows, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t launch_moe_permutation_fwd(const int64_t* topk_indices, int64_t* permute_index,
+                                              int64_t* unpermute_index, int64_t n_tokens, int64_t k,
+                                              int64_t num_experts, void* stream) {
+  if (n_tokens < 0 || k < 0 || num_experts < 1 || num_experts > kPermMaxExperts) return (int32_t)hipErrorInvalidValue;
+  if (k > 0 && n_tokens > INT32_MAX / k) return (int32_t)hipErrorInvalidValue;  // positions are 32-bit
+  const int64_t n = n_tokens * k;
+  if (n == 0) return (int32_t)hipSuccess;
+  const int64_t tiles = (n + kPermThreads - 1) / kPermThreads;
+  const int64_t groups = tiles < kPermMaxGroups ? tiles : kPermMaxGroups;
+  const int64_t chunk = (tiles + groups - 1) / groups * kPermThreads;
+  const unsigned grid = (unsigned)((n + chunk - 1) / chunk);
+  moe_permutation<<<grid, kPermThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      topk_indices, n, k, (int)num_experts, chunk, permute_index, unpermute_index);
+  return launch_status();
 }

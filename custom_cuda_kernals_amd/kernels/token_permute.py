@@ -43,11 +43,22 @@ def token_combine(expert_output: torch.Tensor, unpermute_index: torch.Tensor, we
     return combined
 
 
-def compute_permutation(topk_indices: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+def compute_permutation(topk_indices: torch.Tensor, num_experts: int | None = None
+                        ) -> tuple[torch.Tensor, torch.Tensor]:
     """From ``topk_indices [T, k]`` (expert per token and slot): ``permute_index
     [T*k]`` (source token of each expert-sorted slot; ties keep token order)
-    and ``unpermute_index [T, k]`` (the sorted slot each assignment went to)."""
+    and ``unpermute_index [T, k]`` (the sorted slot each assignment went to).
+
+    With ``num_experts`` (at most 256; ids outside ``[0, num_experts)`` are
+    ordered after every expert) this is one HIP kernel, a stable counting sort;
+    without it, the reference's torch ops (a stable argsort and its inverse,
+    baselines/token_permute.py:55-70) on the tensor's device."""
     t, k = topk_indices.shape
+    if num_experts is not None:
+        permute_index = torch.empty(t * k, dtype=torch.int64, device=topk_indices.device)
+        unpermute_index = torch.empty((t, k), dtype=torch.int64, device=topk_indices.device)
+        native.moe_permutation_fwd(topk_indices, permute_index, unpermute_index, int(num_experts))
+        return permute_index, unpermute_index
     order = torch.argsort(topk_indices.reshape(-1), stable=True)
     permute_index = order // k
     inverse = torch.empty_like(order)

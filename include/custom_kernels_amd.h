@@ -165,6 +165,18 @@ int32_t launch_moe_router_fwd(const void* logits, float* topk_weights, int64_t* 
                               int64_t num_tokens, int64_t num_experts, int64_t k, int32_t dtype,
                               int32_t renormalize, void* stream);
 
+/* The index bookkeeping between the router and the gather: with i indexing
+ * topk_indices int64 [n_tokens, k] flat and entries ordered by (expert id, i),
+ * permute_index int64 [n_tokens * k] gets i / k of the p-th entry and
+ * unpermute_index int64 [n_tokens, k] gets each entry's position p. This is a
+ * stable argsort of the expert ids and its inverse. Ids outside
+ * [0, num_experts) are ordered after every expert, by i. 1 <= num_experts <= 256
+ * and n_tokens * k <= INT32_MAX, else hipErrorInvalidValue.
+ * No reference launcher: replaces the torch ops of reference
+ * baselines/token_permute.py:55-70 (compute_permutation). */
+int32_t launch_moe_permutation_fwd(const int64_t* topk_indices, int64_t* permute_index, int64_t* unpermute_index,
+                                   int64_t n_tokens, int64_t k, int64_t num_experts, void* stream);
+
 /* ---- Diagnostics (no reference counterpart): device-side checks of the
  * arithmetic shortcuts used on the FP8 fast path. ---- */
 

@@ -61,6 +61,8 @@ def test_empty_work_returns_success_without_device_calls():
     assert lib.launch_token_combine_checked_fwd(None, None, None, None, 32, 16, 2, 0, 2, None) == 0
     assert lib.launch_moe_router_fwd(None, None, None, 0, 16, 2, 0, 1, None) == 0
     assert lib.launch_moe_router_fwd(None, None, None, 8, 16, 0, 0, 1, None) == 0
+    assert lib.launch_moe_permutation_fwd(None, None, None, 0, 6, 160, None) == 0
+    assert lib.launch_moe_permutation_fwd(None, None, None, 2048, 0, 160, None) == 0
 
 
 def test_hbm_stream_rejects_bad_arguments_before_device_calls():
@@ -96,6 +98,10 @@ def test_unknown_tags_return_invalid_value_before_device_calls():
     assert lib.launch_moe_router_fwd(None, None, None, 4, 300, 2, 0, 1, None) == 1  # > 256 experts
     assert lib.launch_moe_router_fwd(None, None, None, 4, 8, 9, 0, 1, None) == 1  # k > experts
     assert lib.launch_moe_router_fwd(None, None, None, 4, 8, 2, 5, 1, None) == 1  # bad dtype
+    assert lib.launch_moe_permutation_fwd(None, None, None, 4, 2, 0, None) == 1  # no experts
+    assert lib.launch_moe_permutation_fwd(None, None, None, 4, 2, 257, None) == 1  # > 256 experts
+    assert lib.launch_moe_permutation_fwd(None, None, None, 1 << 30, 8, 16, None) == 1  # positions past 32 bits
+    assert lib.launch_moe_permutation_fwd(None, None, None, -1, 2, 16, None) == 1
 
 
 class _Dev:

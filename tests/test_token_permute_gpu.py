@@ -136,3 +136,89 @@ def test_dispatch_round_trip():
     w = torch.full((t, k), 1.0 / k)
     back = token_combine(permuted, unperm, w.cuda()).cpu()
     torch.testing.assert_close(back, hidden, rtol=1e-6, atol=1e-6)
+
+
+# ---- The permutation bookkeeping as one kernel (compute_permutation with
+# num_experts): a stable counting sort, bit-exact against the oracle's stable
+# argsort (oracle/moe.py compute_permutation, pinned by the reference's own
+# compute_permutation outputs in tests/golden).
+
+def _expected_permutation(topk: np.ndarray, e: int):
+    """The oracle's order with ids outside [0, e) mapped to one bucket after
+    every expert (their relative order, by flat index, is kept)."""
+    ids = np.where((topk >= 0) & (topk < e), topk, e)
+    return moe.compute_permutation(ids)
+
+
+def test_permutation_kernel_golden():
+    import os
+
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "reference_moe.npz"))
+    topk = gold["perm_topk"]
+    perm, unperm = compute_permutation(torch.from_numpy(topk).cuda(), int(topk.max()) + 1)
+    assert np.array_equal(perm.cpu().numpy(), gold["perm_permute"])
+    assert np.array_equal(unperm.cpu().numpy(), gold["perm_unpermute"])
+
+
+@pytest.mark.parametrize("t,k,e", [
+    (2048, 6, 160),    # the router bench shape: 12 workgroups, one tile each
+    (16384, 6, 160),   # 96 tiles over the 64-workgroup cap: two tiles per workgroup
+    (40000, 8, 256),   # 320000 entries: five tiles per workgroup, every bucket of the maximum expert count
+    (257, 3, 8),       # a partial last tile, few experts (long runs of one bucket in a wave)
+    (1, 1, 1), (3, 2, 1), (1025, 1, 2), (64, 8, 64), (511, 4, 255),
+])
+def test_permutation_kernel_matches_oracle(t, k, e):
+    rng = np.random.default_rng(t * 7 + k * 3 + e)
+    topk = rng.integers(0, e, size=(t, k))
+    perm, unperm = compute_permutation(torch.from_numpy(topk).cuda(), e)
+    p_ref, u_ref = moe.compute_permutation(topk)
+    assert perm.dtype == torch.int64 and unperm.shape == (t, k)
+    assert np.array_equal(perm.cpu().numpy(), p_ref)
+    assert np.array_equal(unperm.cpu().numpy(), u_ref)
+
+
+def test_permutation_kernel_skewed_and_router_assignments():
+    """All tokens on one expert (one bucket per wave, the longest runs), and
+    real router output (distinct experts per token)."""
+    t, k, e = 3000, 4, 64
+    topk = np.full((t, k), 17, dtype=np.int64)
+    perm, unperm = compute_permutation(torch.from_numpy(topk).cuda(), e)
+    p_ref, u_ref = moe.compute_permutation(topk)
+    assert np.array_equal(perm.cpu().numpy(), p_ref) and np.array_equal(unperm.cpu().numpy(), u_ref)
+    from custom_cuda_kernals_amd.kernels import moe_router
+
+    logits = inputs.router_inputs(2048, 160, torch.float32, seed=5)
+    _, idx = moe_router(logits.cuda(), 6)
+    perm, unperm = compute_permutation(idx, 160)
+    p_ref, u_ref = moe.compute_permutation(idx.cpu().numpy())
+    assert np.array_equal(perm.cpu().numpy(), p_ref) and np.array_equal(unperm.cpu().numpy(), u_ref)
+
+
+def test_permutation_kernel_out_of_range_ids():
+    """Ids outside [0, num_experts) (negative, too large) are ordered after
+    every expert, by flat index: the outputs stay a permutation, so the gather
+    and combine they feed stay in bounds."""
+    rng = np.random.default_rng(9)
+    t, k, e = 700, 3, 16
+    topk = rng.integers(0, e, size=(t, k))
+    topk[5, 1], topk[77, 0], topk[300, 2], topk[699, 2] = -1, 16, 1 << 40, -(1 << 50)
+    perm, unperm = compute_permutation(torch.from_numpy(topk).cuda(), e)
+    p_ref, u_ref = _expected_permutation(topk, e)
+    assert np.array_equal(perm.cpu().numpy(), p_ref) and np.array_equal(unperm.cpu().numpy(), u_ref)
+    assert sorted(unperm.cpu().numpy().reshape(-1).tolist()) == list(range(t * k))
+
+
+def test_permutation_kernel_rejects_bad_arguments():
+    from custom_cuda_kernals_amd._lib import native
+
+    topk = torch.zeros((4, 2), dtype=torch.int64, device="cuda")
+    p = torch.empty(8, dtype=torch.int64, device="cuda")
+    u = torch.empty((4, 2), dtype=torch.int64, device="cuda")
+    for bad in (0, 257):
+        with pytest.raises(ValueError):
+            native.moe_permutation_fwd(topk, p, u, bad)
+    with pytest.raises(ValueError):
+        native.moe_permutation_fwd(topk, p[:7], u, 8)
+    empty = torch.empty((0, 2), dtype=torch.int64, device="cuda")
+    perm, unperm = compute_permutation(empty, 8)
+    assert perm.numel() == 0 and unperm.shape == (0, 2)
