@@ -112,9 +112,13 @@ def test_rope_in_place_graph():
     _replay_matches_eager([q, k, cos, sin], [q, k], lambda: native.rope_fwd(q, k, cos, sin, q, k), sets)
 
 
-@pytest.mark.parametrize("gran", ["token", "block", "tensor", "static"])
+@pytest.mark.parametrize("gran", ["token", "block", "tensor", "tensor_api", "tensor_api_finish", "static"])
 def test_fp8_quant_graph(gran):
-    m, n = 256, 4096
+    """tensor: the reference ABI (its int32 cleared inside the graph); tensor_api:
+    no amax word, as the Python API calls it (slot arrays in the cast chunks at
+    this size); tensor_api_finish: the same at 2048 rows (one slot array and
+    the finishing launch)."""
+    m, n = (2048 if gran == "tensor_api_finish" else 256), 4096
     sets = [[inputs.fp8_token_input(m, n, BF16, seed=s)] for s in range(3)]
     x = sets[0][0].cuda()
     q = torch.empty(m, n, dtype=F8, device="cuda")
@@ -133,6 +137,9 @@ def test_fp8_quant_graph(gran):
             native.fp8_quant_tensor_fwd(x, q, s, amax, "e4m3")
 
         outs = [q, s, amax]
+    elif gran.startswith("tensor_api"):
+        s = torch.empty(1, device="cuda")
+        launch, outs = (lambda: native.fp8_quant_tensor_fwd(x, q, s, None, "e4m3")), [q, s]
     else:
         launch, outs = (lambda: native.fp8_quant_static_fwd(x, q, 0.05, "e4m3")), [q]
     _replay_matches_eager([x], outs, launch, sets)
@@ -151,3 +158,9 @@ def test_moe_ops_graph():
     lg = sets_r[0][0].cuda()
     tw, ti = torch.empty(512, 6, device="cuda"), torch.empty(512, 6, dtype=torch.int64, device="cuda")
     _replay_matches_eager([lg], [tw, ti], lambda: native.moe_router_fwd(lg, tw, ti, True), sets_r)
+    g = torch.Generator().manual_seed(7)
+    sets_p = [[torch.randint(0, 160, (2048, 6), generator=g)] for _ in range(3)]
+    ids = sets_p[0][0].cuda()
+    perm, unperm = torch.empty(2048 * 6, dtype=torch.int64, device="cuda"), torch.empty(2048, 6, dtype=torch.int64,
+                                                                                          device="cuda")
+    _replay_matches_eager([ids], [perm, unperm], lambda: native.moe_permutation_fwd(ids, perm, unperm, 160), sets_p)
