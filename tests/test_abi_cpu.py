@@ -209,10 +209,32 @@ def test_fp8_checks():
         native.fp8_quant_tensor_fwd(F(4, 8), F(4, 8, dtype=e4), F(1, dtype=torch.float32), F(1, dtype=torch.int64), "e4m3")
     with pytest.raises(ValueError, match="exactly 1 element"):
         native.fp8_quant_tensor_fwd(F(4, 8), F(4, 8, dtype=e4), F(1, dtype=torch.float32), F(2, dtype=torch.int32), "e4m3")
+    # amax_scratch may be None; the other arguments are still checked in order
+    with pytest.raises(ValueError, match="x_fp8 shape"):
+        native.fp8_quant_tensor_fwd(F(4, 8), F(4, 9, dtype=e4), F(1, dtype=torch.float32), None, "e4m3")
+    with pytest.raises(ValueError, match="scale must be float32"):
+        native.fp8_quant_tensor_fwd(F(4, 8), F(4, 8, dtype=e4), F(1), None, "e4m3")
     with pytest.raises(ValueError, match=r"scale shape \[3\] must be \[4\]"):
         native.fp8_quant_token_fwd(F(4, 8), F(4, 8, dtype=e4), F(3, dtype=torch.float32), "e4m3")
     with pytest.raises(ValueError, match="x_fp8 shape"):
         native.fp8_quant_static_fwd(F(4, 8), F(4, 9, dtype=e4), 0.05, "e4m3")
+
+
+def test_moe_permutation_checks():
+    i64 = torch.int64
+    with pytest.raises(ValueError, match="topk_indices must be 2-D"):
+        native.moe_permutation_fwd(F(8, dtype=i64), F(8, dtype=i64), F(8, dtype=i64), 16)
+    with pytest.raises(ValueError, match=r"permute_index shape \[7\] must be \[8\]"):
+        native.moe_permutation_fwd(F(4, 2, dtype=i64), F(7, dtype=i64), F(4, 2, dtype=i64), 16)
+    with pytest.raises(ValueError, match="unpermute_index shape"):
+        native.moe_permutation_fwd(F(4, 2, dtype=i64), F(8, dtype=i64), F(2, 4, dtype=i64), 16)
+    for bad in (0, 257):
+        with pytest.raises(ValueError, match=r"num_experts \(\d+\) must be in \[1, 256\]"):
+            native.moe_permutation_fwd(F(4, 2, dtype=i64), F(8, dtype=i64), F(4, 2, dtype=i64), bad)
+    with pytest.raises(ValueError, match="must be int64"):
+        native.moe_permutation_fwd(F(4, 2, dtype=torch.int32), F(8, dtype=i64), F(4, 2, dtype=i64), 16)
+    with pytest.raises(ValueError, match="must be a CUDA tensor"):
+        kernels.compute_permutation(torch.zeros(4, 2, dtype=i64), 16)
 
 
 def test_fused_checks():
