@@ -172,7 +172,18 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
         if (v < nvec) {
           float fw[VEC];
           C::unpack(rov[k], yv[k]);
-          C::unpack(kHoistW ? wreg[kHoistW ? k : 0] : wv[v], fw);
+          // Where the hoisted weight is unpacked above the row loop (the
+          // optimiser's choice) or kept packed until here (opaque, as in
+          // MODE 0) is picked per shape, measured on MI355X, bf16, unpacked
+          // vs opaque: 512 x 2 per-token 92.9 vs 80.2 us at [8192, 8192],
+          // 64.4 vs 60.1 at [8192, 5120], static 86.6 vs 79.0 at
+          // [8192, 8192]; 1024 x 2 at [4096, 16384] per-token 107.3 vs 105.2,
+          // static 96.9 vs 98.3; 256 x 2 at [16384, 4096] per-token 76.6 vs
+          // 77.0, static 74.6 vs 75.5.
+          constexpr bool kOpaqueW = THREADS == 512 || (THREADS > 512 && MODE == 1);
+          u32x4 wk = kHoistW ? wreg[kHoistW ? k : 0] : wv[v];
+          if constexpr (kOpaqueW) asm("" : "+v"(wk));
+          C::unpack(wk, fw);
           scale_round_mul<C>(yv[k], inv, fw);
 #pragma unroll
           for (int i = 0; i < VEC; i += 2) {
