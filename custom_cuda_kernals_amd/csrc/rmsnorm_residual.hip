@@ -356,25 +356,32 @@ int32_t launch_rmsnorm(const void* x, const void* res, const void* w, void* y, u
     rmsnorm_resident<C, S::kThreads, S::kItems, MODE, FMT><<<g, S::kThreads, 0, st>>>(
         x, res, w, y, yq, scale, ro, rows, cols, eps, static_scale);
   };
-  // Shapes measured on MI355X at cols = 4096 bf16: one vector per thread is
-  // fastest for the plain op (45.0 us against 45.3-46.0 at two per thread);
-  // two per thread for the FP8 variants, whose extra registers (the y values
-  // held across the amax reduction) and extra reduction prefer fewer waves
-  // per row (static scale: 76.2 us against 98.1 at one per thread).
+  // 16-byte rows (f16 / bf16): the shapes come from a sweep over every
+  // THREADS in 64..1024 (step 64) x ITEMS in 1..4 holding the row, on MI355X
+  // at 8192 bf16 rows of 2048..16384 elements (graph-replayed, 2 GiB
+  // rotation). The plain op wants up to 768 threads with one vector each,
+  // then 512 or 768 x 2 and 512 x 4: no 1024-thread shape wins, e.g. 55.5 us
+  // for 768 x 1 at 5120 elements against 81.4 for 1024 x 1, 90.1 for 512 x 2
+  // at 8192 against 108.3, 130.3 for 768 x 2 at 12288 against 155.4. The FP8
+  // variants hold y across the amax reduction and want few waves per row: 256
+  // threads x 1..3 vectors, then 512 x 2..4 (5120 elements: 53.9 us for
+  // 256 x 3 against 60.3 for 512 x 2; 12288: 136.6 for 512 x 3 against 161.3
+  // for 1024 x 2; static 16384: 163.4 for 512 x 4 against 187.4).
   // fp32 rows stage their squares whole in LDS (aten_sum.hpp), so they stop
   // at 1024 x 2 vectors (8192 elements, 32 KB); longer ones loop.
   bool done;
   if constexpr (MODE == 0 && C::VEC == 8) {
-    done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<512, 1>,
-                                    RowShape<1024, 1>, RowShape<1024, 2>,
+    done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<320, 1>,
+                                    RowShape<384, 1>, RowShape<448, 1>, RowShape<512, 1>, RowShape<768, 1>,
+                                    RowShape<512, 2>, RowShape<768, 2>, RowShape<512, 4>,
                                     RowShape<1024, 4>>(nvec, run);
   } else if constexpr (MODE == 0) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<512, 1>,
                                     RowShape<1024, 1>, RowShape<1024, 2>>(nvec, run);
   } else if constexpr (C::VEC == 8) {
-    done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
-                                    RowShape<512, 2>, RowShape<1024, 2>,
-                                    RowShape<1024, 4>>(nvec, run);
+    done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<256, 1>, RowShape<192, 2>,
+                                    RowShape<256, 2>, RowShape<256, 3>, RowShape<512, 2>, RowShape<512, 3>,
+                                    RowShape<512, 4>, RowShape<1024, 4>>(nvec, run);
   } else {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
                                     RowShape<512, 2>, RowShape<1024, 2>>(nvec, run);

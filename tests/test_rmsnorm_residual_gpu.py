@@ -103,7 +103,8 @@ def test_unaligned_and_long_rows(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
-@pytest.mark.parametrize("cols", [64, 512, 1024, 2048, 4096, 8192, 16384, 32768])
+@pytest.mark.parametrize("cols", [64, 512, 1024, 2048, 2056, 2560, 3072, 3584, 4096, 5120, 6144, 6152, 8192, 10240,
+                                  12288, 16384, 32768])
 def test_every_row_shape_bucket(cols, dtype):
     x, r, w = inputs.rmsnorm_inputs(5, cols, dtype, seed=cols)
     _run(x, r, w, 1e-5)
