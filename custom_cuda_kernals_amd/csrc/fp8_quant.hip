@@ -539,9 +539,24 @@ int32_t launch_token(const void* x, uint8_t* q, float* scale, int64_t m, int64_t
     using S = decltype(shape);
     fp8_token_resident<C, FMT, S::kThreads, S::kItems><<<g, S::kThreads, 0, st>>>(x, q, scale, m, n);
   };
-  const bool done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
-                                             RowShape<512, 2>, RowShape<1024, 2>, RowShape<1024, 4>,
-                                             RowShape<1024, 8>>(nvec, run);
+  // 16-byte rows (f16 / bf16) from a sweep over THREADS 64..1024 x ITEMS
+  // 1..4 on MI355X at 8192 bf16 rows of 2048..28672 elements (graph-replayed,
+  // 2 GiB rotation): three or four vectors per thread from 2560 elements on,
+  // e.g. 21.4 us for 256 x 3 at 5120 against 24.2 for 512 x 2, 39.8 for
+  // 512 x 3 at 10240 against 49.0 for 1024 x 2, 63.2 for 512 x 4 at 16384
+  // against 66.3 for 1024 x 2. fp32 rows keep two vectors per thread (27.4
+  // against 28.8 us at [8192, 4096] for 256 x 4).
+  bool done = false;
+  if constexpr (C::VEC == 8) {
+    done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<128, 3>,
+                                    RowShape<256, 2>, RowShape<256, 3>, RowShape<256, 4>, RowShape<512, 3>,
+                                    RowShape<512, 4>, RowShape<1024, 3>, RowShape<1024, 4>,
+                                    RowShape<1024, 8>>(nvec, run);
+  } else {
+    done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
+                                    RowShape<512, 2>, RowShape<1024, 2>, RowShape<1024, 4>,
+                                    RowShape<1024, 8>>(nvec, run);
+  }
   if (!done) fp8_token_generic<C, FMT><<<g, 256, 0, st>>>(x, q, scale, m, n);
   return launch_status();
 }

@@ -300,19 +300,36 @@ bool launch_swiglu_fp8_rows(const void* gate, const void* up, uint8_t* yq, float
   bool launched = false;
   auto run = [&](auto shape) {
     using S = decltype(shape);
-    // The table pays for its per-workgroup fill only on long rows.
-    constexpr bool kTab = std::is_same_v<C, CodecBF16> && S::kThreads == 1024;
-    if constexpr (!STATIC || kTab) {
+    // The table pays for its per-workgroup fill only on long rows. Static
+    // scales use these rows only from 768 threads (the flat stream otherwise).
+    constexpr bool kTab = std::is_same_v<C, CodecBF16> && S::kThreads * S::kItems >= 1152;
+    if constexpr (!STATIC || (kTab && S::kThreads >= 768)) {
       swiglu_fp8_resident<C, S::kThreads, S::kItems, FMT, kTab, STATIC><<<g, S::kThreads, 0, st>>>(
           gate, up, yq, scale, static_scale, rows, cols);
       launched = true;
     }
   };
-  // At most two vectors per thread keeps the kernel under 64 VGPRs of row
-  // state; 1024-thread rows measured fastest on MI355X at cols = 14336 bf16.
+  // bf16 rows from a sweep over THREADS 256..1024 (step 128) x ITEMS 1..4,
+  // with and without the table, on MI355X at 8192 rows of 5632..29568
+  // elements (graph-replayed, 2 GiB rotation): 512 x 2 at 5632 (37.1 us);
+  // 384 x 3 with the table at 8192, 53.4 against 57.6 for 512 x 2; 768 x 2
+  // at 11008, 69.5 against 70.4 for 1024 x 2; 1024 x 2 at 14336 (89.8);
+  // 1024 x 3 at 18944 and 22016, 140.6 / 156.3 against 142.2 / 159.7 for
+  // 1024 x 4 (static scale 122.5 / 137.5 against 128.7 / 148.9). fp16 and
+  // fp32 rows, VALU-bound without the table, keep two vectors per thread
+  // (fp16 at 8192: 56.0 us for 512 x 2 against 62.8 for 384 x 3).
   if (vec_ok) {
-    pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>, RowShape<512, 2>,
-                   RowShape<1024, 2>, RowShape<1024, 4>>(nvec, run);
+    if constexpr (std::is_same_v<C, CodecBF16>) {
+      if (nvec > 896 && nvec <= 1152) {
+        run(RowShape<384, 3>{});
+      } else {
+        pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>, RowShape<512, 2>,
+                       RowShape<768, 2>, RowShape<1024, 2>, RowShape<1024, 3>, RowShape<1024, 4>>(nvec, run);
+      }
+    } else {
+      pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>, RowShape<512, 2>,
+                     RowShape<1024, 2>, RowShape<1024, 4>>(nvec, run);
+    }
   }
   return launched;
 }
