@@ -163,15 +163,24 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
         }
       }
     } else {
-      // y rounded to T and kept as floats; NaN-propagating amax over |y|.
-      float yv[ITEMS][VEC];
+      // y rounded to T; NaN-propagating amax over |y|. Held as floats, or
+      // packed in T (exact: the values are rounded to T already), which
+      // measured on MI355X, bf16, 8192 rows, floats vs packed: per-token
+      // 512 x 4 at 16384 202.3 vs 171.8 us (but 512 x 3 at 12288 135.7 vs
+      // 137.4, 256 x 3 at 5120 53.4 vs 54.1); static 256 x 3 at 5120 54.1 vs
+      // 52.5, 512 x 3 at 12288 124.1 vs 122.1 (but 512 x 4 at 16384 163.5 vs
+      // 166.8).
+      constexpr bool kPackY = (MODE == 1 && ITEMS >= 4) || (MODE == 2 && ITEMS == 3);
+      float yv[kPackY ? 1 : ITEMS][VEC];
+      u32x4 yp[kPackY ? ITEMS : 1];
       float amax = 0.0f;
 #pragma unroll
       for (int k = 0; k < ITEMS; ++k) {
         const int v = threadIdx.x + k * THREADS;
         if (v < nvec) {
           float fw[VEC];
-          C::unpack(rov[k], yv[k]);
+          float f[VEC];
+          C::unpack(rov[k], f);
           // Where the hoisted weight is unpacked above the row loop (the
           // optimiser's choice) or kept packed until here (opaque, as in
           // MODE 0) is picked per shape, measured on MI355X, bf16, unpacked
@@ -184,11 +193,17 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
           u32x4 wk = kHoistW ? wreg[kHoistW ? k : 0] : wv[v];
           if constexpr (kOpaqueW) asm("" : "+v"(wk));
           C::unpack(wk, fw);
-          scale_round_mul<C>(yv[k], inv, fw);
+          scale_round_mul<C>(f, inv, fw);
 #pragma unroll
           for (int i = 0; i < VEC; i += 2) {
-            C::round2(yv[k][i], yv[k][i + 1]);
-            amax = absmax2(amax, yv[k][i], yv[k][i + 1]);
+            C::round2(f[i], f[i + 1]);
+            amax = absmax2(amax, f[i], f[i + 1]);
+          }
+          if constexpr (kPackY) {
+            yp[k] = C::pack(f);
+          } else {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) yv[kPackY ? 0 : k][i] = f[i];
           }
         }
       }
@@ -210,10 +225,17 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
         const int v = threadIdx.x + k * THREADS;
         if (v < nvec) {
           uint32_t wq[VEC / 4];
-          if (fast) {
-            quant_fast<FMT, VEC>(yv[k], s, r, wq);
+          float f[VEC];
+          if constexpr (kPackY) {
+            C::unpack(yp[k], f);
           } else {
-            quant_exact<FMT, VEC>(yv[k], s, wq);
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) f[i] = yv[kPackY ? 0 : k][i];
+          }
+          if (fast) {
+            quant_fast<FMT, VEC>(f, s, r, wq);
+          } else {
+            quant_exact<FMT, VEC>(f, s, wq);
           }
           if constexpr (VEC == 8) {
             bq.st8((u32x2){wq[0], wq[1]}, (uint32_t)v * 8u);
