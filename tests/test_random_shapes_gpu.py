@@ -3,7 +3,7 @@ per-op tests (whose checking helpers are reused here).
 
 The fixed case tables pin the reference's shapes; these cases probe the
 launchers' shape selection instead: row lengths on and around every
-register-resident bucket boundary (in vectors: 64 * 2^i, +-1, +-8 elements),
+register-resident bucket boundary (BUCKET_VECS vectors, +-1, +-8 elements),
 lengths that are not a multiple of the 16-byte vector, single rows and
 columns, and mixed dtypes / FP8 formats. Sizes stay small enough for the CPU
 oracle to finish in a second or two per case.
@@ -27,6 +27,9 @@ from tests.test_token_permute_gpu import _check_combine
 pytestmark = pytest.mark.gpu
 
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+# Row capacities (in 16-byte vectors) of the register-resident shapes of the
+# row kernels (threads x vectors per thread).
+BUCKET_VECS = [64, 128, 192, 256, 320, 384, 448, 512, 768, 896, 1024, 1152, 1536, 2048, 3072, 4096, 8192, 16384]
 N_CASES = 16
 MAX_ELEMS = 1 << 21
 
@@ -38,7 +41,7 @@ def _cols(rng: np.random.Generator, vec: int) -> int:
     if kind == 1:
         return int(vec * rng.integers(1, 2501))
     if kind == 2:  # around a row-shape bucket boundary
-        base = vec * 64 * (1 << int(rng.integers(0, 9)))
+        base = vec * int(rng.choice(BUCKET_VECS))
         return max(1, base + int(rng.choice([-8, -1, 0, 1, 8])))
     return int(rng.integers(1, 65))
 
