@@ -1,0 +1,83 @@
+"""Row kernels whose grid loops: 65536 + 64 rows, so the first 64 workgroups
+take a second row after the grid cap, at row lengths that select every
+register-resident shape of the RMSNorm (+ FP8), per-token FP8 and
+SwiGLU + FP8 launchers (one, two, three and four vectors per thread, the
+weight held across rows, y held packed), against the CPU oracle on the first
+rows, rows in the middle and the rows each looping workgroup took second.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from custom_cuda_kernals_amd.kernels import fp8_quant, rmsnorm_residual, rmsnorm_residual_fp8, swiglu_fp8
+from oracle import eager
+from oracle import fp8 as ofp8
+from tests._parity import assert_codes_equal, assert_f32_bits_equal, bits_equal
+
+pytestmark = pytest.mark.gpu
+
+ROWS = 65536 + 64
+SLICES = [slice(0, 16), slice(30000, 30016), slice(65536, ROWS)]
+
+
+@pytest.fixture(autouse=True)
+def _free_device_memory():
+    yield
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def _randn(shape, seed, dtype=torch.bfloat16):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return torch.randn(shape, dtype=dtype, device="cuda", generator=g)
+
+
+@pytest.mark.parametrize("cols", [5120, 8192, 12288, 16384])
+def test_rmsnorm_rows_loop(cols):
+    x, r = _randn((ROWS, cols), cols), _randn((ROWS, cols), cols + 1)
+    w = (1.0 + 0.1 * _randn((cols,), cols + 2, torch.float32)).to(torch.bfloat16)
+    w_cpu = w.cpu()
+    y, ro = rmsnorm_residual(x, r, w, 1e-5)
+    torch.cuda.synchronize()
+    for sl in SLICES:
+        y_ref, ro_ref = eager.rmsnorm_residual(x[sl].cpu(), r[sl].cpu(), w_cpu, 1e-5)
+        assert bits_equal(ro[sl].cpu(), ro_ref).all(), f"residual_out rows {sl}"
+        assert bits_equal(y[sl].cpu(), y_ref).all(), f"y rows {sl}"
+    del y, ro
+    for static in (None, 0.05):
+        q, s, ro = rmsnorm_residual_fp8(x, r, w, 1e-5, "e4m3", scale=static)
+        torch.cuda.synchronize()
+        for sl in SLICES:
+            codes, s_ref, ro_ref, _ = eager.rmsnorm_residual_fp8(x[sl].cpu(), r[sl].cpu(), w_cpu, 1e-5, "e4m3",
+                                                                 static)
+            assert_codes_equal(q[sl], codes, f"codes rows {sl} static={static}")
+            if static is None:
+                assert_f32_bits_equal(s[sl], s_ref, f"scales rows {sl}")
+            assert bits_equal(ro[sl].cpu(), ro_ref).all(), f"residual_out rows {sl} static={static}"
+        del q, s, ro
+
+
+@pytest.mark.parametrize("cols", [2560, 5120, 10240, 16384, 20480])
+def test_fp8_token_rows_loop(cols):
+    x = _randn((ROWS, cols), cols + 3)
+    q, s = fp8_quant(x, "e4m3", "token")
+    torch.cuda.synchronize()
+    for sl in SLICES:
+        codes, s_ref = ofp8.quant_token(x[sl].float().cpu().numpy(), "e4m3")
+        assert_codes_equal(q[sl], codes, f"codes rows {sl}")
+        assert_f32_bits_equal(s[sl], s_ref, f"scales rows {sl}")
+
+
+@pytest.mark.parametrize("cols", [8192, 12288, 20480])
+@pytest.mark.parametrize("static", [None, 0.05], ids=["token", "static"])
+def test_swiglu_fp8_rows_loop(cols, static):
+    gate, up = _randn((ROWS, cols), cols + 4), _randn((ROWS, cols), cols + 5)
+    q, s = swiglu_fp8(gate, up, "e4m3", scale=static)
+    torch.cuda.synchronize()
+    for sl in SLICES:
+        codes, s_ref, _ = eager.swiglu_fp8(gate[sl].cpu(), up[sl].cpu(), "e4m3", static)
+        assert_codes_equal(q[sl], codes, f"codes rows {sl}")
+        if static is None:
+            assert_f32_bits_equal(s[sl], s_ref, f"scales rows {sl}")
