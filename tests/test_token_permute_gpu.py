@@ -222,3 +222,25 @@ def test_permutation_kernel_rejects_bad_arguments():
     empty = torch.empty((0, 2), dtype=torch.int64, device="cuda")
     perm, unperm = compute_permutation(empty, 8)
     assert perm.numel() == 0 and unperm.shape == (0, 2)
+
+
+@pytest.mark.parametrize("t,k,e,h", [(512, 8, 64, 7168), (300, 2, 8, 4096), (97, 6, 160, 1000)])
+def test_fp8_dispatch_quantise_once_then_gather(t, k, e, h):
+    """The FP8 MoE dispatch: router -> permutation -> per-token FP8 of the T
+    token rows -> gather of their code rows and scales. Equal, bit for bit, to
+    per-token FP8 of the gathered bf16 rows (the scale of a row depends on the
+    row alone), at 3·T·H + 2·k·T·H bytes instead of 3·k·T·H."""
+    from custom_cuda_kernals_amd.kernels import fp8_quant, moe_router
+    from oracle import fp8 as ofp8
+
+    g = torch.Generator().manual_seed(t * k + h)
+    x = torch.randn(t, h, generator=g).to(torch.bfloat16).cuda()
+    logits = torch.randn(t, e, generator=g).cuda()
+    _, ids = moe_router(logits, k)
+    perm, _ = compute_permutation(ids, e)
+    codes, scales = fp8_quant(x, "e4m3", "token")
+    g_codes = token_gather(codes, perm)
+    g_scales = token_gather(scales.view(t, 1), perm).view(-1)
+    ref_codes, ref_scales = ofp8.quant_token(x.cpu()[perm.cpu()].float().numpy(), "e4m3")
+    assert np.array_equal(g_codes.cpu().view(torch.uint8).numpy(), ref_codes)
+    assert np.array_equal(g_scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
