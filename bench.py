@@ -60,6 +60,8 @@ def _parse():
                         "(for counter-collection runs; includes host launch overhead)")
     p.add_argument("--block", action="store_true",
                    help="also time the Llama-3-8B decoder block (eager / fused / fp8) at S=4096")
+    p.add_argument("--block-model", default="llama3-8b", choices=["llama3-8b", "llama3-70b"],
+                   help="layer shapes of the --block decoder block (llama3-70b: hidden 8192, FFN 28672)")
     p.add_argument("--no-ceilings", action="store_true",
                    help="skip the practical-ceiling streams (pure traffic with six config ops' byte patterns)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -525,20 +527,21 @@ def _cpu_baseline(budget_s: float):
             "per_op": per_op}
 
 
-def _block_latency(torch):
-    """Llama-3-8B decoder block, B=1 S=4096 bf16, in the three variants of
+def _block_latency(torch, model="llama3-8b"):
+    """Llama-3 decoder block (the reference's Llama-3-8B, or Llama-3-70B's
+    layer shapes), B=1 S=4096 bf16, in the three variants of
     custom_cuda_kernals_amd.llama_block (the reference's integration proof,
     examples/llama_block.py, with an FP8 variant added)."""
-    from custom_cuda_kernals_amd.llama_block import LlamaBlock, block_latency_ms
+    from custom_cuda_kernals_amd.llama_block import CONFIGS, LlamaBlock, block_latency_ms
 
     torch.manual_seed(0)
-    seq = 4096
-    ref = LlamaBlock(seq, mode="eager").eval()
+    seq, cfg = 4096, CONFIGS[model]
+    ref = LlamaBlock(seq, cfg, mode="eager").eval()
     g = torch.Generator(device="cuda").manual_seed(0)
-    x = torch.randn(1, seq, 4096, dtype=torch.bfloat16, device="cuda", generator=g) * 0.02
-    out = {}
+    x = torch.randn(1, seq, cfg.hidden_size, dtype=torch.bfloat16, device="cuda", generator=g) * 0.02
+    out = {"model": model}
     for mode in ("eager", "fused", "fp8"):
-        blk = ref if mode == "eager" else LlamaBlock(seq, mode=mode).eval()
+        blk = ref if mode == "eager" else LlamaBlock(seq, cfg, mode=mode).eval()
         if blk is not ref:
             blk.load_state_dict(ref.state_dict())
         out[mode] = block_latency_ms(blk, x)
@@ -640,7 +643,7 @@ def main():
     if anchors:
         line["anchors"] = anchors
     if args.block:
-        line["block"] = _block_latency(torch)
+        line["block"] = _block_latency(torch, args.block_model)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = _cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)

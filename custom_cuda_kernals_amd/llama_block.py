@@ -39,7 +39,7 @@ from custom_cuda_kernals_amd.kernels import (
     swiglu_fp8,
 )
 
-__all__ = ["LlamaBlockConfig", "LlamaBlock", "rope_tables", "block_latency_ms", "MODES"]
+__all__ = ["LlamaBlockConfig", "LlamaBlock", "rope_tables", "block_latency_ms", "MODES", "CONFIGS"]
 
 MODES = ("eager", "fused", "fp8")
 
@@ -58,6 +58,14 @@ class LlamaBlockConfig:
     @property
     def head_dim(self) -> int:
         return self.hidden_size // self.num_heads
+
+
+# The reference's block (Llama-3-8B) and, as an addition, Llama-3-70B's layer
+# shapes (config.json: hidden 8192, intermediate 28672, 64 heads, 8 KV heads).
+CONFIGS = {
+    "llama3-8b": LlamaBlockConfig(),
+    "llama3-70b": LlamaBlockConfig(hidden_size=8192, intermediate_size=28672, num_heads=64, num_kv_heads=8),
+}
 
 
 def rope_tables(seq_len: int, head_dim: int, theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:

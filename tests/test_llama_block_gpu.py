@@ -77,6 +77,35 @@ def test_fp8_block_activations_are_the_fused_kernels_codes():
     assert torch.equal(s.view(-1), s2) and torch.equal(ro, ro2)
 
 
+def test_llama3_70b_shaped_blocks_track_eager():
+    """The same gates at Llama-3-70B's layer shapes (hidden 8192, FFN 28672,
+    64 / 8 heads), which take the wide row shapes of the RMSNorm (+ FP8) and
+    SwiGLU (+ FP8) launchers and RoPE with 64 query heads."""
+    from custom_cuda_kernals_amd.llama_block import CONFIGS
+
+    cfg, seq = CONFIGS["llama3-70b"], 256
+    torch.manual_seed(1)
+    ref = LlamaBlock(seq, cfg, mode="eager").eval()
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(1, seq, cfg.hidden_size, dtype=torch.bfloat16, device="cuda", generator=g) * 0.02
+    with torch.no_grad():
+        want = ref(x)
+        for mode in ("fused", "fp8"):
+            blk = LlamaBlock(seq, cfg, mode=mode).eval()
+            blk.load_state_dict(ref.state_dict())
+            got = blk(x)
+            if mode == "fused":
+                _assert_close_with_outliers(got, want, 1e-2, 2e-2, 1e-5)
+            else:
+                upd_ref, upd = want.float() - x.float(), got.float() - x.float()
+                rel = ((upd - upd_ref).norm() / upd_ref.norm()).item()
+                cos = torch.nn.functional.cosine_similarity(upd.flatten(), upd_ref.flatten(), dim=0).item()
+                print(f"\nllama3-70b fp8 block: relative error of the update {rel:.4f}, cosine {cos:.6f}")
+                assert rel < 0.12 and cos > 0.995
+            del blk
+            torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("mode", ["fused", "fp8"])
 def test_block_replays_from_a_hip_graph(mode):
     """The whole block captured once in a HIP graph (this library's kernels,
