@@ -289,7 +289,7 @@ __global__ __launch_bounds__(256) void swiglu_fp8_generic(
 // Register-resident rows: one workgroup per row for the row-length buckets
 // below; false (nothing launched) when no bucket holds the row or the
 // buffers are not aligned for 16-byte access. STATIC rows are used only with
-// the bf16 table (1024-thread rows).
+// the bf16 table and 768 or more threads per row.
 template <class C, int FMT, bool STATIC>
 bool launch_swiglu_fp8_rows(const void* gate, const void* up, uint8_t* yq, float* scale, float static_scale,
                             int64_t rows, int64_t cols, hipStream_t st) {
