@@ -234,6 +234,8 @@ int32_t gather(const void* src, const int64_t* indices, void* dst, int64_t n_dst
   return launch_status();
 }
 
+constexpr int64_t kCombineWideTokens = 4096;
+
 int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, int64_t n_tokens,
                 int64_t k, int64_t h, int32_t dtype, int64_t n_rows, hipStream_t st) {
   if (n_tokens <= 0 || k <= 0 || h <= 0) return (int32_t)hipSuccess;
@@ -245,7 +247,27 @@ int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, 
       // (9.4 us at T=2048, k=2, hidden 4096 bf16); deeper top-k: 2 per thread
       // (20.5 us at k=6); both measured on MI355X against 1-8 vectors and 1-8 rows.
       const int64_t rv = h / C::VEC;
-      if (k <= 2) {
+      auto wide = [&](auto vpl) {
+        constexpr int V = decltype(vpl)::value;
+        token_combine_vec<C, 512, V, 2><<<grid, 512, 0, st>>>(static_cast<const u32x4*>(eo), uidx, w,
+                                                            static_cast<u32x4*>(out), n_tokens, k, rv, n_rows);
+      };
+      if (n_tokens >= kCombineWideTokens && (k <= 2 ? rv >= 512 : rv > 512) && rv <= 4 * 512) {
+        // Many tokens, rows of 4096 to 16384 bf16: 512-thread workgroups
+        // holding the row in one pass, measured on MI355X (graph-replayed)
+        // against the shapes below: 35.0 vs 38.1 us at T=8192, k=2, hidden
+        // 4096 (fp16 34.8 vs 37.2, fp32 66.6 vs 71.5); 186.5 vs 194.3 at
+        // T=8192, k=8, hidden 7168; 412.7 vs 437.2 at hidden 16384 (but 10.4
+        // vs 9.2 at T=2048, k=2, hidden 4096, 27.2 vs 26.3 at T=4096, k=8,
+        // hidden 2048, and 159.5 vs 158.5 at T=16384, k=6, hidden 4096).
+        if (rv <= 512) {
+          wide(IntC<1>{});
+        } else if (rv <= 1024) {
+          wide(IntC<2>{});
+        } else {
+          wide(IntC<4>{});
+        }
+      } else if (k <= 2) {
         with_row_threads<4, 128>(rv, [&](auto threads) {
           constexpr int TH = decltype(threads)::value;
           token_combine_vec<C, TH, 4, 2><<<grid, TH, 0, st>>>(static_cast<const u32x4*>(eo), uidx, w,

@@ -244,3 +244,23 @@ def test_fp8_dispatch_quantise_once_then_gather(t, k, e, h):
     ref_codes, ref_scales = ofp8.quant_token(x.cpu()[perm.cpu()].float().numpy(), "e4m3")
     assert np.array_equal(g_codes.cpu().view(torch.uint8).numpy(), ref_codes)
     assert np.array_equal(g_scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("k,h", [(2, 4096), (8, 7168), (2, 16384), (6, 4096), (8, 5120)])
+def test_combine_many_tokens(k, h, dtype):
+    """4100 tokens: the 512-thread one-pass shape for rows of 4096-16384
+    elements (and the default shapes beside it), checked on token slices at
+    the start, the middle and the end against the explicit j-order sum."""
+    t = 4100
+    g = torch.Generator(device="cuda").manual_seed(k * h)
+    eo = torch.randn(t * k, h, device="cuda", generator=g).to(dtype)
+    ui = torch.randperm(t * k, device="cuda", generator=g).view(t, k)
+    w = torch.rand(t, k, device="cuda", generator=g)
+    out = token_combine(eo, ui, w)
+    torch.cuda.synchronize()
+    for sl in (slice(0, 24), slice(2000, 2024), slice(t - 24, t)):
+        rows = ui[sl].reshape(-1)
+        local = torch.arange(rows.numel()).view(-1, k)
+        ref = moe.combine_sequential(eo[rows].cpu(), local, w[sl].cpu())
+        assert bits_equal(out[sl].cpu(), ref).all(), sl
