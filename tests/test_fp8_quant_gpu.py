@@ -119,7 +119,7 @@ def test_unaligned_input_pointer(gran, dtype):
     _check(x_cpu, "e4m3", gran, x_dev=x_dev)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("cols", [64, 512, 1024, 2048, 2560, 3072, 4096, 5120, 6144, 8192, 10240, 12288, 16384, 20480,
                                   24576, 32768, 65536])
 def test_every_row_shape_bucket(cols, dtype):

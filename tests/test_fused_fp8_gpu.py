@@ -110,7 +110,7 @@ BUCKET_COLS = [64, 512, 1024, 2048, 2056, 2560, 3072, 3584, 4096, 5120, 6144, 61
                16384, 20480, 32768]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("cols", BUCKET_COLS)
 def test_every_row_shape_bucket(cols, dtype):
     x, r, w = inputs.rmsnorm_inputs(3, cols, dtype, seed=cols)

@@ -102,7 +102,7 @@ def test_unaligned_and_long_rows(dtype):
     _run(x[:3, :1000].contiguous(), r[:3, :1000].contiguous(), w[:1000].contiguous(), 1e-5, xd, rd)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("cols", [64, 512, 1024, 2048, 2056, 2560, 3072, 3584, 4096, 5120, 6144, 6152, 8192, 10240,
                                   12288, 16384, 32768])
 def test_every_row_shape_bucket(cols, dtype):
