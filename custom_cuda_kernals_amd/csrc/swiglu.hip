@@ -315,9 +315,12 @@ bool launch_swiglu_fp8_rows(const void* gate, const void* up, uint8_t* yq, float
   // 384 x 3 with the table at 8192, 53.4 against 57.6 for 512 x 2; 768 x 2
   // at 11008, 69.5 against 70.4 for 1024 x 2; 1024 x 2 at 14336 (89.8);
   // 1024 x 3 at 18944 and 22016, 140.6 / 156.3 against 142.2 / 159.7 for
-  // 1024 x 4 (static scale 122.5 / 137.5 against 128.7 / 148.9). fp16 and
-  // fp32 rows, VALU-bound without the table, keep two vectors per thread
-  // (fp16 at 8192: 56.0 us for 512 x 2 against 62.8 for 384 x 3).
+  // 1024 x 4 (static scale 122.5 / 137.5 against 128.7 / 148.9). fp16 rows
+  // (no table, VALU-bound, and at 68 VGPRs a 1024 x 2 workgroup is alone on
+  // its CU) from the same sweep: 768 x 2 at 11008, 78.9 against 113.2 us for
+  // 1024 x 2; 512 x 4 at 14336, 100.6 against 125.9; 1024 x 3 at 18944,
+  // 166.3 against 170.7; 256 x 3 at 5632, 39.5 against 41.0; 512 x 2 at 8192
+  // (57.5; 62.8 for 384 x 3). fp32 rows keep two vectors per thread.
   if (vec_ok) {
     if constexpr (std::is_same_v<C, CodecBF16>) {
       if (nvec > 896 && nvec <= 1152) {
@@ -326,6 +329,10 @@ bool launch_swiglu_fp8_rows(const void* gate, const void* up, uint8_t* yq, float
         pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>, RowShape<512, 2>,
                        RowShape<768, 2>, RowShape<1024, 2>, RowShape<1024, 3>, RowShape<1024, 4>>(nvec, run);
       }
+    } else if constexpr (std::is_same_v<C, CodecF16>) {
+      pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>, RowShape<256, 3>,
+                     RowShape<512, 2>, RowShape<768, 2>, RowShape<512, 4>, RowShape<1024, 3>,
+                     RowShape<1024, 4>>(nvec, run);
     } else {
       pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>, RowShape<512, 2>,
                      RowShape<1024, 2>, RowShape<1024, 4>>(nvec, run);
