@@ -389,8 +389,9 @@ int32_t launch_rmsnorm(const void* x, const void* res, const void* w, void* y, u
   // threads x 1..3 vectors, then 512 x 2..4 (5120 elements: 53.9 us for
   // 256 x 3 against 60.3 for 512 x 2; 12288: 136.6 for 512 x 3 against 161.3
   // for 1024 x 2; static 16384: 163.4 for 512 x 4 against 187.4).
-  // fp32 rows stage their squares whole in LDS (aten_sum.hpp), so they stop
-  // at 1024 x 2 vectors (8192 elements, 32 KB); longer ones loop.
+  // fp32 rows stage their squares whole in LDS (aten_sum.hpp): up to
+  // 1024 x 4 vectors (16384 elements, 64 KB of the 160 KB a gfx950
+  // workgroup may hold); longer ones loop.
   bool done;
   if constexpr (MODE == 0 && C::VEC == 8) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<320, 1>,
@@ -399,14 +400,16 @@ int32_t launch_rmsnorm(const void* x, const void* res, const void* w, void* y, u
                                     RowShape<1024, 4>>(nvec, run);
   } else if constexpr (MODE == 0) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<512, 1>,
-                                    RowShape<1024, 1>, RowShape<1024, 2>>(nvec, run);
+                                    RowShape<1024, 1>, RowShape<1024, 2>, RowShape<1024, 3>,
+                                    RowShape<1024, 4>>(nvec, run);
   } else if constexpr (C::VEC == 8) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<256, 1>, RowShape<192, 2>,
                                     RowShape<256, 2>, RowShape<256, 3>, RowShape<512, 2>, RowShape<512, 3>,
                                     RowShape<512, 4>, RowShape<1024, 4>>(nvec, run);
   } else {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
-                                    RowShape<512, 2>, RowShape<1024, 2>>(nvec, run);
+                                    RowShape<512, 2>, RowShape<1024, 2>, RowShape<1024, 3>,
+                                    RowShape<1024, 4>>(nvec, run);
   }
   if (!done) {
     rmsnorm_generic<C, MODE, FMT><<<g, 256, 0, st>>>(x, res, w, y, yq, scale, ro, rows, cols, eps, static_scale);
