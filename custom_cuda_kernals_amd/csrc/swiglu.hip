@@ -165,11 +165,15 @@ constexpr int kPolQ = kPolSC1 | kPolNT;
 // selects the LDS SiLU table, filled while the first row's loads are in
 // flight. STATIC uses static_scale and skips the row reduction; each thread's
 // own max |y| then selects the fast or exact conversion for its vectors.
-template <class C, int THREADS, int ITEMS, int FMT, bool TAB, bool STATIC>
+// LDSY (rows of more than four vectors per thread): y is parked in LDS, in
+// slots only its own thread reads back, instead of registers; 1024 x 8
+// vectors hold rows of 65536 bf16 / fp16 (32768 fp32) elements in 128 KB.
+template <class C, int THREADS, int ITEMS, int FMT, bool TAB, bool STATIC, bool LDSY = false>
 __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
     const void* __restrict__ gate, const void* __restrict__ up, uint8_t* __restrict__ yq,
     float* __restrict__ scale, float static_scale, int64_t rows, int64_t cols) {
   constexpr int NW = THREADS / 64;
+  __shared__ u32x4 ylds[LDSY ? THREADS * ITEMS : 1];
   constexpr int VEC = C::VEC;
   __shared__ uint32_t lds[2 * NW];
   __shared__ __attribute__((aligned(16))) float tab[TAB ? SiluTableBF16::kEntries : 1];
@@ -201,22 +205,24 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
     __syncthreads();
   }
   for (; row < rows; row += gridDim.x) {
-    float y[ITEMS][VEC];
+    float y[LDSY ? 1 : ITEMS][VEC];
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       const int v = threadIdx.x + k * THREADS;
       if (v < nvec) {
         float u[VEC];
-        silu_vec<C, TAB>(graw[k], tab, y[k]);
+        float(&yk)[VEC] = y[LDSY ? 0 : k];
+        silu_vec<C, TAB>(graw[k], tab, yk);
         C::unpack(uraw[k], u);
 #pragma unroll
         for (int i = 0; i < VEC; i += 2) {
-          y[k][i] = y[k][i] * u[i];
-          y[k][i + 1] = y[k][i + 1] * u[i + 1];
-          C::round2(y[k][i], y[k][i + 1]);
-          amax = absmax2(amax, y[k][i], y[k][i + 1]);
+          yk[i] = yk[i] * u[i];
+          yk[i + 1] = yk[i + 1] * u[i + 1];
+          C::round2(yk[i], yk[i + 1]);
+          amax = absmax2(amax, yk[i], yk[i + 1]);
         }
+        if constexpr (LDSY) ylds[k * THREADS + threadIdx.x] = C::pack(y[0]);
       }
     }
     float s;
@@ -241,10 +247,12 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
       const uint32_t v = threadIdx.x + k * THREADS;
       if (v < (uint32_t)nvec) {
         uint32_t wq[VEC / 4];
+        float(&yk)[VEC] = y[LDSY ? 0 : k];
+        if constexpr (LDSY) C::unpack(ylds[k * THREADS + threadIdx.x], y[0]);
         if (fast) {
-          quant_fast<FMT, VEC>(y[k], s, r, wq);
+          quant_fast<FMT, VEC>(yk, s, r, wq);
         } else {
-          quant_exact<FMT, VEC>(y[k], s, wq);
+          quant_exact<FMT, VEC>(yk, s, wq);
         }
         if constexpr (VEC == 8) {
           bq.st8((u32x2){wq[0], wq[1]}, v * 8u);
@@ -303,8 +311,9 @@ bool launch_swiglu_fp8_rows(const void* gate, const void* up, uint8_t* yq, float
     // The table pays for its per-workgroup fill only on long rows. Static
     // scales use these rows only from 768 threads (the flat stream otherwise).
     constexpr bool kTab = std::is_same_v<C, CodecBF16> && S::kThreads * S::kItems >= 1152;
-    if constexpr (!STATIC || (kTab && S::kThreads >= 768)) {
-      swiglu_fp8_resident<C, S::kThreads, S::kItems, FMT, kTab, STATIC><<<g, S::kThreads, 0, st>>>(
+    constexpr bool kLdsY = S::kItems > 4;
+    if constexpr (!STATIC || (kTab && S::kThreads >= 768 && !kLdsY)) {
+      swiglu_fp8_resident<C, S::kThreads, S::kItems, FMT, kTab, STATIC, kLdsY><<<g, S::kThreads, 0, st>>>(
           gate, up, yq, scale, static_scale, rows, cols);
       launched = true;
     }
@@ -327,15 +336,16 @@ bool launch_swiglu_fp8_rows(const void* gate, const void* up, uint8_t* yq, float
         run(RowShape<384, 3>{});
       } else {
         pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>, RowShape<512, 2>,
-                       RowShape<768, 2>, RowShape<1024, 2>, RowShape<1024, 3>, RowShape<1024, 4>>(nvec, run);
+                       RowShape<768, 2>, RowShape<1024, 2>, RowShape<1024, 3>, RowShape<1024, 4>,
+                       RowShape<1024, 6>, RowShape<1024, 8>>(nvec, run);
       }
     } else if constexpr (std::is_same_v<C, CodecF16>) {
       pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>, RowShape<256, 3>,
                      RowShape<512, 2>, RowShape<768, 2>, RowShape<512, 4>, RowShape<1024, 3>,
-                     RowShape<1024, 4>>(nvec, run);
+                     RowShape<1024, 4>, RowShape<1024, 6>, RowShape<1024, 8>>(nvec, run);
     } else {
       pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>, RowShape<512, 2>,
-                     RowShape<1024, 2>, RowShape<1024, 4>>(nvec, run);
+                     RowShape<1024, 2>, RowShape<1024, 4>, RowShape<1024, 6>, RowShape<1024, 8>>(nvec, run);
     }
   }
   return launched;

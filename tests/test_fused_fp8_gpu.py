@@ -107,7 +107,7 @@ def test_swiglu_fp8_small(shape, dtype, fmt, static):
 # Row lengths that reach every register-resident shape of both kernels (the
 # largest row each shape holds, and one vector past some of them).
 BUCKET_COLS = [64, 512, 1024, 2048, 2056, 2560, 3072, 3584, 4096, 5120, 6144, 6152, 7176, 8192, 9216, 10240, 12288,
-               16384, 20480, 32768]
+               16384, 20480, 24576, 32768, 40960, 53248, 65536]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])

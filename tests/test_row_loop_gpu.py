@@ -1,9 +1,10 @@
 """Row kernels whose grid loops: 65536 + 64 rows, so the first 64 workgroups
 take a second row after the grid cap, at row lengths that select every
 register-resident shape of the RMSNorm (+ FP8), per-token FP8 and
-SwiGLU + FP8 launchers (one, two, three and four vectors per thread, the
-weight held across rows, y held packed), against the CPU oracle on the first
-rows, rows in the middle and the rows each looping workgroup took second.
+SwiGLU + FP8 launchers (one to four vectors per thread, the weight held
+across rows, y held packed, y parked in LDS for rows of 53248), against the
+CPU oracle on the first rows, rows in the middle and the rows each looping
+workgroup took second.
 """
 
 from __future__ import annotations
@@ -70,7 +71,7 @@ def test_fp8_token_rows_loop(cols):
         assert_f32_bits_equal(s[sl], s_ref, f"scales rows {sl}")
 
 
-@pytest.mark.parametrize("cols", [8192, 12288, 20480])
+@pytest.mark.parametrize("cols", [8192, 12288, 20480, 53248])
 @pytest.mark.parametrize("static", [None, 0.05], ids=["token", "static"])
 def test_swiglu_fp8_rows_loop(cols, static):
     gate, up = _randn((ROWS, cols), cols + 4), _randn((ROWS, cols), cols + 5)
