@@ -90,7 +90,10 @@ __global__ __launch_bounds__(THREADS) void fp8_token_resident(const void* __rest
   // entry, before the loop set-up, and each next row's before the current
   // one is reduced. 6.0 vs 6.3-6.5 us at [2048, 4096] bf16 on MI355X against
   // loading inside the loop (where each load also waited for the one before
-  // it to feed the max).
+  // it to feed the max). Rows of more than four vectors per thread issue the
+  // next row's loads after the current row's stores instead, so the two rows
+  // do not hold registers at once.
+  constexpr bool kAhead = ITEMS <= 4;
   u32x4 nxt[ITEMS];
   auto issue = [&](int64_t row) {
     const RowBuf<true> bx(static_cast<const char*>(x) + row * cols * C::kBytes, row_bytes);
@@ -105,7 +108,7 @@ __global__ __launch_bounds__(THREADS) void fp8_token_resident(const void* __rest
     u32x4 raw[ITEMS];
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) raw[k] = nxt[k];
-    if (row + gridDim.x < rows) issue(row + gridDim.x);
+    if (kAhead && row + gridDim.x < rows) issue(row + gridDim.x);
     uint32_t acc = 0;
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
@@ -139,6 +142,7 @@ __global__ __launch_bounds__(THREADS) void fp8_token_resident(const void* __rest
         }
       }
     }
+    if (!kAhead && row + gridDim.x < rows) issue(row + gridDim.x);
   }
 }
 
@@ -550,7 +554,7 @@ int32_t launch_token(const void* x, uint8_t* q, float* scale, int64_t m, int64_t
   if constexpr (C::VEC == 8) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<128, 3>,
                                     RowShape<256, 2>, RowShape<256, 3>, RowShape<256, 4>, RowShape<512, 3>,
-                                    RowShape<512, 4>, RowShape<1024, 3>, RowShape<1024, 4>,
+                                    RowShape<512, 4>, RowShape<1024, 3>, RowShape<1024, 4>, RowShape<1024, 6>,
                                     RowShape<1024, 8>>(nvec, run);
   } else {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,

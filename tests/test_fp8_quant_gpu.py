@@ -121,7 +121,7 @@ def test_unaligned_input_pointer(gran, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("cols", [64, 512, 1024, 2048, 2560, 3072, 4096, 5120, 6144, 8192, 10240, 12288, 16384, 20480,
-                                  24576, 32768, 65536])
+                                  24576, 32768, 40960, 49152, 65536])
 def test_every_row_shape_bucket(cols, dtype):
     _check(inputs.randn((3, cols), dtype, seed=cols), "e4m3", "token")
 

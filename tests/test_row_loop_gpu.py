@@ -60,7 +60,7 @@ def test_rmsnorm_rows_loop(cols):
         del q, s, ro
 
 
-@pytest.mark.parametrize("cols", [2560, 5120, 10240, 16384, 20480])
+@pytest.mark.parametrize("cols", [2560, 5120, 10240, 16384, 20480, 40960, 65536])
 def test_fp8_token_rows_loop(cols):
     x = _randn((ROWS, cols), cols + 3)
     q, s = fp8_quant(x, "e4m3", "token")
