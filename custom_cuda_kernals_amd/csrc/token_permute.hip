@@ -253,9 +253,9 @@ int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, 
                                                             static_cast<u32x4*>(out), n_tokens, k, rv, n_rows);
       };
       if (n_tokens >= kCombineWideTokens && (k <= 2 ? rv >= 512 : rv > 512) && rv <= 4 * 512) {
-        // Many tokens, rows of 4096 to 16384 bf16: 512-thread workgroups
-        // holding the row in one pass, measured on MI355X (graph-replayed)
-        // against the shapes below: 35.0 vs 38.1 us at T=8192, k=2, hidden
+        // Many tokens, rows of 512 to 2048 vectors (4096 to 16384 bf16):
+        // 512-thread workgroups holding the row in one pass, measured on
+        // MI355X (graph-replayed) against the shapes below: 35.0 vs 38.1 us at T=8192, k=2, hidden
         // 4096 (fp16 34.8 vs 37.2, fp32 66.6 vs 71.5); 186.5 vs 194.3 at
         // T=8192, k=8, hidden 7168; 412.7 vs 437.2 at hidden 16384 (but 10.4
         // vs 9.2 at T=2048, k=2, hidden 4096, 27.2 vs 26.3 at T=4096, k=8,
