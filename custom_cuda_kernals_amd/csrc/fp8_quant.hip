@@ -548,7 +548,8 @@ int32_t launch_token(const void* x, uint8_t* q, float* scale, int64_t m, int64_t
   // 2 GiB rotation): three or four vectors per thread from 2560 elements on,
   // e.g. 21.4 us for 256 x 3 at 5120 against 24.2 for 512 x 2, 39.8 for
   // 512 x 3 at 10240 against 49.0 for 1024 x 2, 63.2 for 512 x 4 at 16384
-  // against 66.3 for 1024 x 2. fp32 rows keep two vectors per thread (27.4
+  // against 66.3 for 1024 x 2; 1024 x 6 at 36864, 74.5 against 91.3 for
+  // 1024 x 8. fp32 rows keep two vectors per thread up to 1024 x 2 (27.4
   // against 28.8 us at [8192, 4096] for 256 x 4).
   bool done = false;
   if constexpr (C::VEC == 8) {

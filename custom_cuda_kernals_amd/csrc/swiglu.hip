@@ -329,7 +329,8 @@ bool launch_swiglu_fp8_rows(const void* gate, const void* up, uint8_t* yq, float
   // its CU) from the same sweep: 768 x 2 at 11008, 78.9 against 113.2 us for
   // 1024 x 2; 512 x 4 at 14336, 100.6 against 125.9; 1024 x 3 at 18944,
   // 166.3 against 170.7; 256 x 3 at 5632, 39.5 against 41.0; 512 x 2 at 8192
-  // (57.5; 62.8 for 384 x 3). fp32 rows keep two vectors per thread.
+  // (57.5; 62.8 for 384 x 3). fp32 rows keep two vectors per thread up to
+  // 1024 x 2. Wider rows of every type take 1024 x 6 or 8 with y in LDS.
   if (vec_ok) {
     if constexpr (std::is_same_v<C, CodecBF16>) {
       if (nvec > 896 && nvec <= 1152) {
