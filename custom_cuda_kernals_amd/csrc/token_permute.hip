@@ -295,23 +295,10 @@ constexpr int64_t kNoBound = INT64_MAX;
 // flattened [T, k] expert ids and its inverse):
 //   permute_index[p]   = i / k for the i-th entry in (expert, i) order
 //   unpermute_index[i] = p, its position in that order.
-// Expert ids are bounded, so this is a stable counting sort in one launch.
-// Entries whose id lies outside [0, n_experts) go to one extra bucket after
-// every expert (so the outputs stay a permutation of [0, n)).
-//
-// G workgroups (at most kPermMaxGroups), workgroup c owning entries
-// [c * chunk, (c + 1) * chunk) in tiles of kPermThreads:
-//   1. every workgroup counts all n ids per bucket in LDS, those before its
-//      chunk (before) and the others (after), one LDS atomic per id:
-//      base[b] = (ids in buckets below b) + before[b];
-//   2. per tile, every lane ORs its lane bit into its wave's mask of its
-//      bucket (LDS); the bits below a lane in its own mask rank it among the
-//      wave's lanes of the same bucket, the popcounts of the lower waves'
-//      masks offset it, so ties keep index order; a running count per bucket
-//      carries the order from tile to tile.
-// Each workgroup reads all n ids once more than a per-chunk count would, so
-// the grid is capped: at n = 12288 (2048 tokens, top 6) that is 12 workgroups
-// and 1.2 MB of L2 reads.
+// Expert ids are bounded, so this is a stable counting sort: one launch
+// below kPermSplitMin entries, three from there on. Entries whose id lies
+// outside [0, n_experts) go to one extra bucket after every expert (so the
+// outputs stay a permutation of [0, n)).
 // ---------------------------------------------------------------------------
 constexpr int kPermThreads = 1024, kPermWaves = kPermThreads / 64;
 constexpr int kPermMaxExperts = 256, kPermBuckets = kPermMaxExperts + 1;
@@ -322,20 +309,110 @@ __device__ inline uint32_t lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+__device__ inline int perm_bucket(int64_t id, int n_experts) {
+  return (id >= 0 && id < n_experts) ? (int)id : n_experts;
+}
+
+// hist[key] += 1 for every active lane, in one LDS atomic per wave. The lanes
+// whose key equals the first active lane's add once, through that lane: a
+// skewed routing puts most of a wave's ids on one expert, and LDS atomics on
+// one address serialise.
+__device__ inline void perm_count(uint32_t* hist, int key) {
+  const int key0 = __builtin_amdgcn_readfirstlane(key);
+  const unsigned long long same = __ballot(key == key0);
+  const bool other = key != key0;
+  if (other || lanes_below(same) == 0u) atomicAdd(&hist[key], other ? 1u : (uint32_t)__popcll(same));
+}
+
+// Wave 0 turns the bucket counts (before + after this workgroup's chunk)
+// into each bucket's first position for the chunk:
+// base[b] = (entries in buckets below b) + before[b].
+// Lane l holds buckets [l * kPermPerLane, (l + 1) * kPermPerLane).
+__device__ inline void perm_bases(const uint32_t* after, const uint32_t* before, uint32_t* base, int nb, int lane) {
+  uint32_t loc[kPermPerLane], sum = 0u;
+#pragma unroll
+  for (int i = 0; i < kPermPerLane; ++i) {
+    const int b = lane * kPermPerLane + i;
+    loc[i] = b < nb ? before[b] + after[b] : 0u;
+    sum += loc[i];
+  }
+  uint32_t incl = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  uint32_t run = incl - sum;
+#pragma unroll
+  for (int i = 0; i < kPermPerLane; ++i) {
+    const int b = lane * kPermPerLane + i;
+    if (b < nb) base[b] = run + before[b];
+    run += loc[i];
+  }
+}
+
+// Stable ranking of the entries [c0, c1) from base[]: per tile, every lane
+// ORs its lane bit into its wave's mask of its bucket; the bits below a lane
+// in its own mask rank it among the wave's lanes of the same bucket, the
+// popcounts of the lower waves' masks offset it, so ties keep index order; a
+// running count per bucket carries the order from tile to tile.
+// lane_mask must be zero on entry and is zero on return.
+template <bool kWritePermute>
+__device__ inline void perm_rank_chunk(const int64_t* __restrict__ ids, int64_t k, int n_experts, int64_t c0,
+                                       int64_t c1, uint32_t* base, unsigned long long (*lane_mask)[kPermBuckets],
+                                       int64_t* __restrict__ permute_index, int64_t* __restrict__ unpermute_index) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb = n_experts + 1;
+  for (int64_t t0 = c0; t0 < c1; t0 += kPermThreads) {
+    const int64_t j = t0 + tid;
+    const bool valid = j < c1;
+    const int b = valid ? perm_bucket(ids[j], n_experts) : 0;
+    if (valid) atomicOr(&lane_mask[wave][b], 1ull << lane);
+    __syncthreads();
+    if (valid) {
+      uint32_t pos = base[b] + lanes_below(lane_mask[wave][b]);
+      for (int w = 0; w < wave; ++w) pos += (uint32_t)__popcll(lane_mask[w][b]);
+      if constexpr (kWritePermute) permute_index[pos] = j / k;
+      unpermute_index[j] = pos;
+    }
+    __syncthreads();
+    // Carry this tile's counts into base and clear the masks for the next tile.
+    for (int i = tid; i < nb; i += kPermThreads) {
+      uint32_t c = 0u;
+#pragma unroll
+      for (int w = 0; w < kPermWaves; ++w) {
+        c += (uint32_t)__popcll(lane_mask[w][i]);
+        lane_mask[w][i] = 0ull;
+      }
+      base[i] += c;
+    }
+    __syncthreads();
+  }
+}
+
+// One launch: workgroup c owns the entries [c * chunk, (c + 1) * chunk) in
+// tiles of kPermThreads, and counts all n ids per bucket in LDS, those before
+// its chunk (before) and the others (after), one LDS atomic per id. Each
+// workgroup reads all n ids once more than a per-chunk count would, so the
+// grid is capped: at n = 12288 (2048 tokens, top 6) that is 12 workgroups and
+// 1.2 MB of L2 reads. kCombine counts through perm_count; it is used for
+// k <= 2 only: with more picks per token (distinct experts per token), a
+// wave's 64 entries hold at most 64 / k of any one expert, and the combining
+// step costs more than it saves (6.9 against 6.0 us at 2048 tokens x top 6).
+template <bool kCombine>
 __global__ __launch_bounds__(kPermThreads) void moe_permutation(const int64_t* __restrict__ ids, int64_t n, int64_t k,
                                                                 int n_experts, int64_t chunk,
                                                                 int64_t* __restrict__ permute_index,
                                                                 int64_t* __restrict__ unpermute_index) {
-  __shared__ uint32_t after[kPermBuckets], before[kPermBuckets], base[kPermBuckets];
+  // before = sides[0], after = sides[1]
+  __shared__ uint32_t sides[2 * kPermBuckets], base[kPermBuckets];
   __shared__ unsigned long long lane_mask[kPermWaves][kPermBuckets];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  uint32_t* before = sides;
+  uint32_t* after = sides + kPermBuckets;
+  const int tid = threadIdx.x;
   const int nb = n_experts + 1;
-  auto bucket = [&](int64_t id) { return (id >= 0 && id < n_experts) ? (int)id : n_experts; };
-  for (int i = tid; i < nb; i += kPermThreads) {
-    after[i] = 0u;
-    before[i] = 0u;
-  }
+  for (int i = tid; i < 2 * kPermBuckets; i += kPermThreads) sides[i] = 0u;
   for (int i = tid; i < kPermWaves * kPermBuckets; i += kPermThreads) (&lane_mask[0][0])[i] = 0ull;
   __syncthreads();
   const int64_t c0 = (int64_t)blockIdx.x * chunk;
@@ -353,60 +430,109 @@ __global__ __launch_bounds__(kPermThreads) void moe_permutation(const int64_t* _
     for (int u = 0; u < kPermUnroll; ++u) {
       const int64_t j = j0 + (int64_t)u * kPermThreads;
       if (j < n) {
-        atomicAdd(j < c0 ? &before[bucket(v[u])] : &after[bucket(v[u])], 1u);
+        const int key = perm_bucket(v[u], n_experts) + (j < c0 ? 0 : kPermBuckets);
+        if constexpr (kCombine) {
+          perm_count(sides, key);
+        } else {
+          atomicAdd(&sides[key], 1u);
+        }
       }
     }
   }
   __syncthreads();
-  if (wave == 0) {
-    // Exclusive scan of the bucket totals: lane l holds buckets
-    // [l * kPermPerLane, (l + 1) * kPermPerLane).
-    uint32_t loc[kPermPerLane], sum = 0u;
+  if (tid < 64) perm_bases(after, before, base, nb, tid);
+  __syncthreads();
+  perm_rank_chunk<true>(ids, k, n_experts, c0, c1, base, lane_mask, permute_index, unpermute_index);
+}
+
+// Three launches from kPermSplitMin entries on, so that each id is counted
+// once: the cost of the one-launch kernel grows with n x workgroups (uniform
+// ids, top 8 of 256: 14.0 against 22.9 us at 16384 tokens, 26.4 against 81.2
+// at 65536; the one launch is faster up to 49152 entries). The output
+// buffers carry the intermediate results between the launches (stream order
+// separates them):
+//   1. moe_permutation_count: workgroup c counts its own chunk per bucket and
+//      stores the counts in permute_index's memory as uint32 [G][nb];
+//   2. moe_permutation_rank: workgroup c sums the counts of the chunks before
+//      its own (before) and of the others (after), then ranks its chunk as the
+//      one-launch kernel does and writes unpermute_index only;
+//   3. moe_permutation_invert: permute_index[unpermute_index[i]] = i / k,
+//      overwriting the counts.
+// The G x nb x 4 bytes of counts fit in permute_index's n x 8 bytes, since
+// G <= n / kPermSplitChunk + 1 and nb <= kPermBuckets.
+constexpr int64_t kPermSplitMin = 65536, kPermSplitChunk = 2048;
+constexpr int kPermSplitMaxGroups = 256;
+
+__global__ __launch_bounds__(kPermThreads) void moe_permutation_count(const int64_t* __restrict__ ids, int64_t n,
+                                                                      int n_experts, int64_t chunk,
+                                                                      uint32_t* __restrict__ counts) {
+  __shared__ uint32_t hist[kPermBuckets];
+  const int tid = threadIdx.x;
+  const int nb = n_experts + 1;
+  for (int i = tid; i < nb; i += kPermThreads) hist[i] = 0u;
+  __syncthreads();
+  const int64_t c0 = (int64_t)blockIdx.x * chunk;
+  const int64_t c1 = c0 + chunk < n ? c0 + chunk : n;
+  for (int64_t j0 = c0 + tid; j0 < c1; j0 += (int64_t)kPermThreads * kPermUnroll) {
+    int64_t v[kPermUnroll];
 #pragma unroll
-    for (int i = 0; i < kPermPerLane; ++i) {
-      const int b = lane * kPermPerLane + i;
-      loc[i] = b < nb ? before[b] + after[b] : 0u;
-      sum += loc[i];
+    for (int u = 0; u < kPermUnroll; ++u) {
+      const int64_t j = j0 + (int64_t)u * kPermThreads;
+      v[u] = j < c1 ? ids[j] : 0;
     }
-    uint32_t incl = sum;
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t o = __shfl_up(incl, d);
-      if (lane >= d) incl += o;
-    }
-    uint32_t run = incl - sum;
-#pragma unroll
-    for (int i = 0; i < kPermPerLane; ++i) {
-      const int b = lane * kPermPerLane + i;
-      if (b < nb) base[b] = run + before[b];
-      run += loc[i];
+    for (int u = 0; u < kPermUnroll; ++u) {
+      if (j0 + (int64_t)u * kPermThreads < c1) perm_count(hist, perm_bucket(v[u], n_experts));
     }
   }
   __syncthreads();
-  for (int64_t t0 = c0; t0 < c1; t0 += kPermThreads) {
-    const int64_t j = t0 + tid;
-    const bool valid = j < c1;
-    const int b = valid ? bucket(ids[j]) : 0;
-    if (valid) atomicOr(&lane_mask[wave][b], 1ull << lane);
-    __syncthreads();
-    if (valid) {
-      uint32_t pos = base[b] + lanes_below(lane_mask[wave][b]);
-      for (int w = 0; w < wave; ++w) pos += (uint32_t)__popcll(lane_mask[w][b]);
-      permute_index[pos] = j / k;
-      unpermute_index[j] = pos;
-    }
-    __syncthreads();
-    // Carry this tile's counts into base and clear the masks for the next tile.
-    for (int i = tid; i < nb; i += kPermThreads) {
-      uint32_t c = 0u;
+  for (int i = tid; i < nb; i += kPermThreads) counts[(int64_t)blockIdx.x * nb + i] = hist[i];
+}
+
+__global__ __launch_bounds__(kPermThreads) void moe_permutation_rank(const int64_t* __restrict__ ids, int64_t n,
+                                                                     int64_t k, int n_experts, int64_t chunk,
+                                                                     const uint32_t* __restrict__ counts,
+                                                                     int64_t* __restrict__ unpermute_index) {
+  __shared__ uint32_t after[kPermBuckets], before[kPermBuckets], base[kPermBuckets];
+  __shared__ unsigned long long lane_mask[kPermWaves][kPermBuckets];
+  const int tid = threadIdx.x;
+  const int nb = n_experts + 1;
+  for (int i = tid; i < nb; i += kPermThreads) {
+    after[i] = 0u;
+    before[i] = 0u;
+  }
+  for (int i = tid; i < kPermWaves * kPermBuckets; i += kPermThreads) (&lane_mask[0][0])[i] = 0ull;
+  __syncthreads();
+  // counts[g][b] for every chunk g: flat index i = g * nb + b, coalesced
+  // (at most kPermSplitMaxGroups x kPermBuckets of them, so 32-bit).
+  const uint32_t n_counts = gridDim.x * (uint32_t)nb, mine = blockIdx.x * (uint32_t)nb;
+  for (uint32_t i0 = tid; i0 < n_counts; i0 += kPermThreads * kPermUnroll) {
+    uint32_t v[kPermUnroll];
 #pragma unroll
-      for (int w = 0; w < kPermWaves; ++w) {
-        c += (uint32_t)__popcll(lane_mask[w][i]);
-        lane_mask[w][i] = 0ull;
-      }
-      base[i] += c;
+    for (int u = 0; u < kPermUnroll; ++u) {
+      const uint32_t i = i0 + u * kPermThreads;
+      v[u] = i < n_counts ? counts[i] : 0u;
     }
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kPermUnroll; ++u) {
+      const uint32_t i = i0 + u * kPermThreads;
+      if (i < n_counts && v[u] != 0u) atomicAdd(i < mine ? &before[i % nb] : &after[i % nb], v[u]);
+    }
+  }
+  __syncthreads();
+  if (tid < 64) perm_bases(after, before, base, nb, tid);
+  __syncthreads();
+  const int64_t c0 = (int64_t)blockIdx.x * chunk;
+  const int64_t c1 = c0 + chunk < n ? c0 + chunk : n;
+  perm_rank_chunk<false>(ids, k, n_experts, c0, c1, base, lane_mask, nullptr, unpermute_index);
+}
+
+__global__ __launch_bounds__(256) void moe_permutation_invert(const int64_t* __restrict__ unpermute_index, int64_t n,
+                                                              int64_t k, int64_t* __restrict__ permute_index) {
+  // n < 2^31 (the launcher's bound), so the token index is a 32-bit quotient.
+  const uint32_t kk = (uint32_t)k;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    permute_index[unpermute_index[i]] = (int64_t)((uint32_t)i / kk);
   }
 }
 
@@ -451,11 +577,34 @@ extern "C" int32_t launch_moe_permutation_fwd(const int64_t* topk_indices, int64
   if (k > 0 && n_tokens > INT32_MAX / k) return (int32_t)hipErrorInvalidValue;  // positions are 32-bit
   const int64_t n = n_tokens * k;
   if (n == 0) return (int32_t)hipSuccess;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n >= kPermSplitMin) {
+    int64_t chunk = kPermSplitChunk;
+    if ((n + chunk - 1) / chunk > kPermSplitMaxGroups) {
+      chunk = (n + kPermSplitMaxGroups - 1) / kPermSplitMaxGroups;
+      chunk = (chunk + kPermThreads - 1) / kPermThreads * kPermThreads;
+    }
+    const unsigned groups = (unsigned)((n + chunk - 1) / chunk);
+    // The counts ([groups][nb] uint32) live in permute_index until the last launch.
+    uint32_t* counts = reinterpret_cast<uint32_t*>(permute_index);
+    moe_permutation_count<<<groups, kPermThreads, 0, st>>>(topk_indices, n, (int)num_experts, chunk, counts);
+    moe_permutation_rank<<<groups, kPermThreads, 0, st>>>(topk_indices, n, k, (int)num_experts, chunk, counts,
+                                                          unpermute_index);
+    const int64_t blocks = (n + 255) / 256;
+    moe_permutation_invert<<<(unsigned)(blocks < 2048 ? blocks : 2048), 256, 0, st>>>(unpermute_index, n, k,
+                                                                                     permute_index);
+    return launch_status();
+  }
   const int64_t tiles = (n + kPermThreads - 1) / kPermThreads;
   const int64_t groups = tiles < kPermMaxGroups ? tiles : kPermMaxGroups;
   const int64_t chunk = (tiles + groups - 1) / groups * kPermThreads;
   const unsigned grid = (unsigned)((n + chunk - 1) / chunk);
-  moe_permutation<<<grid, kPermThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      topk_indices, n, k, (int)num_experts, chunk, permute_index, unpermute_index);
+  if (k <= 2) {
+    moe_permutation<true><<<grid, kPermThreads, 0, st>>>(topk_indices, n, k, (int)num_experts, chunk, permute_index,
+                                                         unpermute_index);
+  } else {
+    moe_permutation<false><<<grid, kPermThreads, 0, st>>>(topk_indices, n, k, (int)num_experts, chunk,
+                                                          permute_index, unpermute_index);
+  }
   return launch_status();
 }

@@ -164,3 +164,10 @@ def test_moe_ops_graph():
     perm, unperm = torch.empty(2048 * 6, dtype=torch.int64, device="cuda"), torch.empty(2048, 6, dtype=torch.int64,
                                                                                           device="cuda")
     _replay_matches_eager([ids], [perm, unperm], lambda: native.moe_permutation_fwd(ids, perm, unperm, 160), sets_p)
+    # 16384 x 8 entries: the three-launch permutation (counts kept in permute_index between launches)
+    sets_q = [[torch.randint(0, 256, (16384, 8), generator=g)] for _ in range(3)]
+    ids_q = sets_q[0][0].cuda()
+    perm_q = torch.empty(16384 * 8, dtype=torch.int64, device="cuda")
+    unperm_q = torch.empty(16384, 8, dtype=torch.int64, device="cuda")
+    _replay_matches_eager([ids_q], [perm_q, unperm_q],
+                          lambda: native.moe_permutation_fwd(ids_q, perm_q, unperm_q, 256), sets_q)

@@ -162,10 +162,14 @@ def test_permutation_kernel_golden():
 
 @pytest.mark.parametrize("t,k,e", [
     (2048, 6, 160),    # the router bench shape: 12 workgroups, one tile each
-    (16384, 6, 160),   # 96 tiles over the 64-workgroup cap: two tiles per workgroup
-    (40000, 8, 256),   # 320000 entries: five tiles per workgroup, every bucket of the maximum expert count
+    (8191, 8, 256),    # 65528 entries, the largest one-launch size: 64 workgroups
+    (65535, 1, 3),     # the largest one-launch size with k = 1 (wave-combined counts)
+    (8192, 8, 256),    # 65536 entries, the smallest three-launch size: 32 chunks of 2048
+    (40000, 8, 256),   # 320000 entries (three launches): a partial last chunk, every bucket of the maximum expert count
+    (131072, 8, 256),  # 1048576 entries: 256 chunks of 4096
+    (70001, 2, 8),     # three launches, k = 2, few experts
     (257, 3, 8),       # a partial last tile, few experts (long runs of one bucket in a wave)
-    (1, 1, 1), (3, 2, 1), (1025, 1, 2), (64, 8, 64), (511, 4, 255),
+    (1, 1, 1), (3, 2, 1), (1025, 1, 2), (64, 8, 64), (511, 4, 255), (30000, 2, 8),
 ])
 def test_permutation_kernel_matches_oracle(t, k, e):
     rng = np.random.default_rng(t * 7 + k * 3 + e)
@@ -178,13 +182,18 @@ def test_permutation_kernel_matches_oracle(t, k, e):
 
 
 def test_permutation_kernel_skewed_and_router_assignments():
-    """All tokens on one expert (one bucket per wave, the longest runs), and
+    """All tokens on one expert (one bucket per wave, the longest runs), most
+    tokens on one expert, at one- and three-launch sizes and k = 1 / 2 / 4, and
     real router output (distinct experts per token)."""
-    t, k, e = 3000, 4, 64
-    topk = np.full((t, k), 17, dtype=np.int64)
-    perm, unperm = compute_permutation(torch.from_numpy(topk).cuda(), e)
-    p_ref, u_ref = moe.compute_permutation(topk)
-    assert np.array_equal(perm.cpu().numpy(), p_ref) and np.array_equal(unperm.cpu().numpy(), u_ref)
+    rng = np.random.default_rng(3)
+    for t, k, e in ((3000, 4, 64), (3000, 1, 64), (12000, 2, 8), (90000, 1, 64), (40000, 4, 64)):
+        topk = np.full((t, k), 17 % e, dtype=np.int64)
+        mixed = np.where(rng.random((t, k)) < 0.9, 5, rng.integers(0, e, size=(t, k)))
+        for ids in (topk, mixed):
+            perm, unperm = compute_permutation(torch.from_numpy(ids).cuda(), e)
+            p_ref, u_ref = moe.compute_permutation(ids)
+            assert np.array_equal(perm.cpu().numpy(), p_ref), (t, k, e)
+            assert np.array_equal(unperm.cpu().numpy(), u_ref), (t, k, e)
     from custom_cuda_kernals_amd.kernels import moe_router
 
     logits = inputs.router_inputs(2048, 160, torch.float32, seed=5)
@@ -199,13 +208,15 @@ def test_permutation_kernel_out_of_range_ids():
     every expert, by flat index: the outputs stay a permutation, so the gather
     and combine they feed stay in bounds."""
     rng = np.random.default_rng(9)
-    t, k, e = 700, 3, 16
-    topk = rng.integers(0, e, size=(t, k))
-    topk[5, 1], topk[77, 0], topk[300, 2], topk[699, 2] = -1, 16, 1 << 40, -(1 << 50)
-    perm, unperm = compute_permutation(torch.from_numpy(topk).cuda(), e)
-    p_ref, u_ref = _expected_permutation(topk, e)
-    assert np.array_equal(perm.cpu().numpy(), p_ref) and np.array_equal(unperm.cpu().numpy(), u_ref)
-    assert sorted(unperm.cpu().numpy().reshape(-1).tolist()) == list(range(t * k))
+    for t, k, e in ((700, 3, 16), (30000, 3, 16)):  # one launch, three launches
+        topk = rng.integers(0, e, size=(t, k))
+        topk[5, 1], topk[77, 0], topk[300, 2], topk[699, 2] = -1, 16, 1 << 40, -(1 << 50)
+        if t > 700:
+            topk[rng.random((t, k)) < 0.01] = e + 3
+        perm, unperm = compute_permutation(torch.from_numpy(topk).cuda(), e)
+        p_ref, u_ref = _expected_permutation(topk, e)
+        assert np.array_equal(perm.cpu().numpy(), p_ref) and np.array_equal(unperm.cpu().numpy(), u_ref)
+        assert np.array_equal(np.sort(unperm.cpu().numpy().reshape(-1)), np.arange(t * k))
 
 
 def test_permutation_kernel_rejects_bad_arguments():
