@@ -171,7 +171,10 @@ int32_t launch_moe_router_fwd(const void* logits, float* topk_weights, int64_t* 
  * unpermute_index int64 [n_tokens, k] gets each entry's position p. This is a
  * stable argsort of the expert ids and its inverse. Ids outside
  * [0, num_experts) are ordered after every expert, by i. 1 <= num_experts <= 256
- * and n_tokens * k <= INT32_MAX, else hipErrorInvalidValue.
+ * and n_tokens * k <= INT32_MAX, else hipErrorInvalidValue. From 65536
+ * entries the call enqueues three kernels on stream and keeps intermediate
+ * counts in permute_index until the last one; the three buffers must not
+ * overlap.
  * No reference launcher: replaces the torch ops of reference
  * baselines/token_permute.py:55-70 (compute_permutation). */
 int32_t launch_moe_permutation_fwd(const int64_t* topk_indices, int64_t* permute_index, int64_t* unpermute_index,
