@@ -3,6 +3,7 @@
 // unknown tag, returned before any device call; the launch status otherwise).
 #pragma once
 
+#include <atomic>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -82,6 +83,33 @@ constexpr unsigned kLdsForGroupsPerCu = (160u * 1024u * 2u) / (2u * N + 1u);
 static_assert(3 * kLdsForGroupsPerCu<3> <= 160u * 1024u && 4 * kLdsForGroupsPerCu<3> > 160u * 1024u);
 static_assert(6 * kLdsForGroupsPerCu<6> <= 160u * 1024u && 7 * kLdsForGroupsPerCu<6> > 160u * 1024u);
 static_assert(kLdsForGroupsPerCu<3> <= 64u * 1024u);  // within the default per-workgroup limit
+
+// Workgroups of KERNEL (launched with `threads` threads and no dynamic LDS)
+// that the current device holds at once: occupancy per CU x CUs, looked up
+// once per kernel and device; 0 when a query fails.
+template <auto KERNEL>
+int64_t resident_groups(int threads) {
+  constexpr int kDevices = 64;
+  static std::atomic<int> cache[kDevices] = {};  // -1 = the query failed
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevices) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  int g = cache[dev].load(std::memory_order_relaxed);
+  if (g == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, KERNEL, threads, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu * cus <= 0) {
+      (void)hipGetLastError();
+      g = -1;
+    } else {
+      g = per_cu * cus;
+    }
+    cache[dev].store(g, std::memory_order_relaxed);
+  }
+  return g > 0 ? g : 0;
+}
 
 inline unsigned flat_grid(int64_t work_items, int threads, int64_t cap) {
   int64_t g = (work_items + threads - 1) / threads;

@@ -158,6 +158,18 @@ def test_every_bf16_gate_fused_table_rows():
         _check_swiglu(g, u, "e4m3", static)
 
 
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("shape", [(600, 40960), (300, 65536), (257, 53248), (1000, 36872)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_swiglu_fp8_bf16_lds_rows_every_row(shape, fmt):
+    """bf16 rows with y parked in LDS run on a grid of the workgroups the
+    device holds at once (one per CU), each looping over rows with the next
+    row's loads issued before the amax reduction: every row checked, grids
+    that loop once, twice and with a partial last round."""
+    g, u = inputs.swiglu_inputs(*shape, torch.bfloat16, seed=shape[0])
+    _check_swiglu(g, u, fmt, None)
+
+
 @pytest.mark.parametrize("static", [None, 0.05])
 @pytest.mark.parametrize("shape", [(77, 14336), (9, 20008), (130, 8200)], ids=lambda s: f"{s[0]}x{s[1]}")
 def test_swiglu_fp8_table_paths_ragged(shape, static):

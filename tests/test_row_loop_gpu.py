@@ -71,6 +71,31 @@ def test_fp8_token_rows_loop(cols):
         assert_f32_bits_equal(s[sl], s_ref, f"scales rows {sl}")
 
 
+@pytest.mark.parametrize("dtype,cols", [(torch.float16, 40960), (torch.float32, 24576)], ids=["fp16", "fp32"])
+def test_swiglu_fp8_lds_rows_loop(dtype, cols):
+    """fp16 / fp32 rows with y parked in LDS (1024 x 6 vectors), whose next
+    row's loads go out before the amax reduction once the grid loops."""
+    gate, up = _randn((ROWS, cols), cols + 6, dtype), _randn((ROWS, cols), cols + 7, dtype)
+    q, s = swiglu_fp8(gate, up, "e4m3")
+    y = None
+    if dtype == torch.float32:
+        from custom_cuda_kernals_amd.kernels import swiglu
+
+        y = swiglu(gate[SLICES[-1]], up[SLICES[-1]])
+    torch.cuda.synchronize()
+    for sl in SLICES:
+        if dtype == torch.float32:
+            if sl is not SLICES[-1]:
+                continue
+            # fp32: the codes quantise the library's own SwiGLU output (torch-CPU's fp32
+            # sigmoid is not correctly rounded; test_fused_fp8_gpu.py states the bar)
+            codes, s_ref = ofp8.quant_token(y.cpu().numpy(), "e4m3")
+        else:
+            codes, s_ref, _ = eager.swiglu_fp8(gate[sl].cpu(), up[sl].cpu(), "e4m3", None)
+        assert_codes_equal(q[sl], codes.reshape(q[sl].shape), f"codes rows {sl}")
+        assert_f32_bits_equal(s[sl], s_ref.reshape(s[sl].shape), f"scales rows {sl}")
+
+
 @pytest.mark.parametrize("cols", [8192, 12288, 20480, 53248])
 @pytest.mark.parametrize("static", [None, 0.05], ids=["token", "static"])
 def test_swiglu_fp8_rows_loop(cols, static):
