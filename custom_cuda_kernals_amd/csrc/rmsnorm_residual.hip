@@ -375,8 +375,18 @@ int32_t launch_rmsnorm(const void* x, const void* res, const void* w, void* y, u
   const unsigned g = row_grid(rows);
   auto run = [&](auto shape) {
     using S = decltype(shape);
-    rmsnorm_resident<C, S::kThreads, S::kItems, MODE, FMT><<<g, S::kThreads, 0, st>>>(
-        x, res, w, y, yq, scale, ro, rows, cols, eps, static_scale);
+    // Wide FP8 rows run on a grid of the workgroups the device holds at once,
+    // each looping over rows (no idle CU between rows, one weight load per
+    // workgroup): per-token from 1536 vectors of capacity (8192 bf16 rows:
+    // 126.9 against 134.6 us at 12288 columns, 286.1 against 301.5 at 24576;
+    // fp16 172.8 against 184.9 at 16384), static from 3072 (273.3 against
+    // 297.7 at 24576). Plain RMSNorm rows lose 3-6 % on such a grid.
+    constexpr auto kernel = rmsnorm_resident<C, S::kThreads, S::kItems, MODE, FMT>;
+    constexpr int kCap = S::kThreads * S::kItems;
+    constexpr bool kLoop = (MODE == 1 && kCap >= 1536) || (MODE == 2 && kCap >= 3072);
+    const int64_t resident = kLoop ? resident_groups<kernel>(S::kThreads) : 0;
+    const unsigned grid = resident > 0 && resident < (int64_t)g ? (unsigned)resident : g;
+    kernel<<<grid, S::kThreads, 0, st>>>(x, res, w, y, yq, scale, ro, rows, cols, eps, static_scale);
   };
   // 16-byte rows (f16 / bf16): the shapes come from a sweep over every
   // THREADS in 64..1024 (step 64) x ITEMS in 1..4 holding the row, on MI355X

@@ -158,6 +158,19 @@ def test_every_bf16_gate_fused_table_rows():
         _check_swiglu(g, u, "e4m3", static)
 
 
+@pytest.mark.parametrize("static", [None, 0.05])
+@pytest.mark.parametrize("dtype,shape", [
+    (torch.bfloat16, (1000, 12288)), (torch.bfloat16, (700, 16384)), (torch.bfloat16, (600, 24576)),
+    (torch.bfloat16, (300, 32768)), (torch.float16, (700, 16384)), (torch.float32, (900, 8192)),
+    (torch.float32, (500, 16384))], ids=lambda v: str(v).split(".")[-1] if isinstance(v, torch.dtype) else f"{v[0]}x{v[1]}")
+def test_rmsnorm_fp8_wide_rows_every_row(dtype, shape, static):
+    """Wide RMSNorm + FP8 rows run on a grid of the workgroups the device
+    holds at once, each looping over rows with the weight held: every row
+    checked, with grids that loop once or more and a partial last round."""
+    x, r, w = inputs.rmsnorm_inputs(*shape, dtype, seed=shape[1] + 1)
+    _check_rms(x, r, w, 1e-5, "e4m3", static)
+
+
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
 @pytest.mark.parametrize("shape", [(600, 40960), (300, 65536), (257, 53248), (1000, 36872)],
                          ids=lambda s: f"{s[0]}x{s[1]}")
