@@ -99,13 +99,10 @@ int64_t resident_groups(int threads) {
   int g = cache[dev].load(std::memory_order_relaxed);
   if (g == 0) {
     int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, KERNEL, threads, 0) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu * cus <= 0) {
-      (void)hipGetLastError();
-      g = -1;
-    } else {
-      g = per_cu * cus;
-    }
+    const bool ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, KERNEL, threads, 0) == hipSuccess &&
+                    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess;
+    if (!ok) (void)hipGetLastError();  // a failed query must not surface as the launch's status
+    g = ok && per_cu * cus > 0 ? per_cu * cus : -1;
     cache[dev].store(g, std::memory_order_relaxed);
   }
   return g > 0 ? g : 0;
