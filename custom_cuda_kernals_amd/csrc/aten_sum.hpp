@@ -177,6 +177,40 @@ __device__ inline float aten_finish(const AtenSumPlan& pl, const float* bs, cons
   return aten_combine(pl, q, tail, lane);
 }
 
+// The same finish for a row of exactly NB whole regions (n = 512 * NB, so
+// nv = 64 NB, steps = 16 NB, P = 4 up to 2^24 addends, and no trailing
+// steps, leftover vectors or trailing scalars), with every count known at
+// compile time: the cascade is unrolled and no tail words are read. The
+// result is the same bits as aten_finish for that n.
+template <int NB>
+__device__ inline float aten_finish_full(const float* bs, int lane) {
+  float q = 0.0f;
+  if (lane < kFoldLanes) {
+    float f[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) f[b] = bs[b * kFoldLanes + lane];
+    if constexpr (NB <= 16) {
+      q = f[0];
+#pragma unroll
+      for (int b = 1; b < NB; ++b) q = q + f[b];
+    } else {
+      // FoldCascade's operations with the block indices unrolled.
+      FoldCascade cs;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) cs.add(f[b], b, 4);
+      q = cs.a1;
+      if constexpr (NB >= 16) q = q + cs.a2;
+      if constexpr (NB >= 256) q = q + cs.a3;
+    }
+  }
+  const float q1 = swizzle_xor<8>(q), q2 = swizzle_xor<16>(q), q3 = swizzle_xor<24>(q);
+  const float p = ((q + q1) + q2) + q3;
+  float t = readlane_f32(p, 0);
+#pragma unroll
+  for (int l = 1; l < kSumLanes; ++l) t = t + readlane_f32(p, l);
+  return t;
+}
+
 // Copy the leftover vectors and trailing scalars that fall in a staged region
 // (first vector `first_vec` of the row) to the tail words.
 __device__ inline void stage_tail_parts(const AtenSumPlan& pl, const float* a, int64_t first_vec, int lane,
@@ -208,12 +242,17 @@ __device__ inline void stage_tail_parts(const AtenSumPlan& pl, const float* a, i
 // `bsum` holds 2 x NREG x 32 floats and `tail` 2 x 64, alternated by `parity`
 // so a wave running ahead into the next row never overwrites words that a
 // slower wave still reads.
-template <int VEC, int THREADS, int ITEMS>
+//   FULL (VEC == 8 only): the row is exactly THREADS * ITEMS vectors and a
+//     whole number of regions, so every count is a compile-time constant and
+//     no tail is staged (aten_finish_full).
+template <int VEC, int THREADS, int ITEMS, bool FULL = false>
 struct ResidentRowSum {
   static constexpr int NW = THREADS / 64;
   static constexpr int NREG = (THREADS * ITEMS * VEC + kRegionAddends - 1) / kRegionAddends;
   static constexpr int SLOTS = (ITEMS >= 2 && NW <= 8) ? 2 : 1;
   static constexpr int kStageFloats = VEC == 8 ? NW * SLOTS * kRegionAddends : THREADS * ITEMS * VEC;
+  static_assert(!FULL || (VEC == 8 && (THREADS * ITEMS * VEC) % kRegionAddends == 0),
+                "a full row is whole regions of 8-lane vectors");
   const AtenSumPlan& pl;
   float* stage;
   float* bs;
@@ -223,11 +262,11 @@ struct ResidentRowSum {
       : pl(plan), stage(stage_), bs(bsum + parity * NREG * kFoldLanes), tl(tail + parity * kTailWords) {
     lane = threadIdx.x & 63;
     w = threadIdx.x >> 6;
-    nreg = (int)pl.nfull + (pl.has_tail() ? 1 : 0);
+    nreg = FULL ? NREG : (int)pl.nfull + (pl.has_tail() ? 1 : 0);
   }
   // Fold region `reg` staged at `a`, as fold c (c < 32) of this lane.
   __device__ void fold_one(const float* a, int reg, int c) {
-    if (reg < pl.nfull) {
+    if (FULL || reg < pl.nfull) {
       bs[reg * kFoldLanes + c] = fold_region16(a, c);
     } else {
       tl[c] = fold_region(a, pl.ntrail, c, 0.0f);
@@ -236,7 +275,7 @@ struct ResidentRowSum {
   }
   __device__ void item(int k, const float (&sq)[VEC]) {
     if constexpr (VEC == 8) {
-      if (w + NW * k < nreg) {
+      if (FULL || w + NW * k < nreg) {
         float* a = stage + (w * SLOTS + k % SLOTS) * kRegionAddends;
 #pragma unroll
         for (int i = 0; i < VEC; ++i) a[lane * VEC + i] = sq[i];
@@ -248,7 +287,7 @@ struct ResidentRowSum {
         __builtin_amdgcn_wave_barrier();
         const int h = lane >> 5;
         const int kk = k - k % SLOTS + h;  // the item this half folds
-        if (kk < ITEMS && (SLOTS == 2 || h == 0) && w + NW * kk < nreg) {
+        if (kk < ITEMS && (SLOTS == 2 || h == 0) && (FULL || w + NW * kk < nreg)) {
           fold_one(stage + (w * SLOTS + h) * kRegionAddends, w + NW * kk, lane & 31);
         }
         __builtin_amdgcn_wave_barrier();
@@ -268,7 +307,11 @@ struct ResidentRowSum {
       }
     }
     __syncthreads();
-    return aten_finish<NREG>(pl, bs, tl, lane);
+    if constexpr (FULL) {
+      return aten_finish_full<NREG>(bs, lane);
+    } else {
+      return aten_finish<NREG>(pl, bs, tl, lane);
+    }
   }
 };
 

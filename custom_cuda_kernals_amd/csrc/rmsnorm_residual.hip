@@ -50,20 +50,29 @@ __device__ inline void scale_round_mul(float (&f)[C::VEC], float inv, const floa
 // grid limit loop with a stride of gridDim.x). A persistent grid (a few
 // workgroups per CU, each prefetching its next row while reducing the
 // current one) measured about 3 % slower on MI355X than a workgroup per row.
-template <class C, int THREADS, int ITEMS, int MODE, int FMT>
+//
+// FULL: the row is exactly THREADS * ITEMS vectors and a whole number of
+// 512-addend regions (bf16 / fp16 at 4096 columns: configs 2 and 5a), so the
+// row length, the per-vector bounds checks and the whole summation plan are
+// compile-time constants. Measured on MI355X at [16384, 4096] bf16,
+// per-token FP8: see the launcher.
+template <class C, int THREADS, int ITEMS, int MODE, int FMT, bool FULL>
 __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
     const void* __restrict__ x, const void* __restrict__ res, const void* __restrict__ w,
     void* __restrict__ y, uint8_t* __restrict__ yq, float* __restrict__ scale,
-    void* __restrict__ ro, int64_t rows, int64_t cols, float eps, float static_scale) {
+    void* __restrict__ ro, int64_t rows, int64_t cols_arg, float eps, float static_scale) {
   constexpr int NW = THREADS / 64;
   constexpr int VEC = C::VEC;
   constexpr int NREG = (THREADS * ITEMS * VEC + kRegionAddends - 1) / kRegionAddends;
   __shared__ uint32_t lds[2 * NW];
-  using RowSum = ResidentRowSum<VEC, THREADS, ITEMS>;
+  using RowSum = ResidentRowSum<VEC, THREADS, ITEMS, FULL>;
   __shared__ float sum_stage[RowSum::kStageFloats];
   __shared__ float sum_blocks[2 * NREG * kFoldLanes];
-  __shared__ float sum_tail[2 * kTailWords];
+  __shared__ float sum_tail[FULL ? 1 : 2 * kTailWords];
+  const int64_t cols = FULL ? (int64_t)THREADS * ITEMS * VEC : cols_arg;
   const int nvec = (int)(cols / VEC);
+  // Vector v of the row exists (always, for a full row).
+  auto in_row = [&](uint32_t v) { return FULL || v < (uint32_t)nvec; };
   const AtenSumPlan plan(cols);
   const u32x4* wv = static_cast<const u32x4*>(w);
   const uint32_t row_bytes = (uint32_t)(cols * C::kBytes);
@@ -74,7 +83,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       const uint32_t v = threadIdx.x + k * THREADS;
-      if (v < (uint32_t)nvec) {
+      if (in_row(v)) {
         xa[k] = bx.ld16(v * 16u);
         ra[k] = br.ld16(v * 16u);
       }
@@ -91,7 +100,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       const int v = threadIdx.x + k * THREADS;
-      if (v < nvec) wreg[k] = wv[v];
+      if (in_row(v)) wreg[k] = wv[v];
     }
   }
   // A workgroup's first row is loaded at kernel entry, ahead of the loop
@@ -117,7 +126,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
       float sq[VEC];
 #pragma unroll
       for (int i = 0; i < VEC; ++i) sq[i] = 0.0f;
-      if (v < nvec) {
+      if (in_row(v)) {
         float fx[VEC], fr[VEC], fo[VEC];
         C::unpack(xa[k], fx);
         C::unpack(ra[k], fr);
@@ -148,7 +157,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
 #pragma unroll
       for (int k = 0; k < ITEMS; ++k) {
         const int v = threadIdx.x + k * THREADS;
-        if (v < nvec) {
+        if (in_row(v)) {
           float fo[VEC], fw[VEC];
           C::unpack(rov[k], fo);
           // Opaque to the optimiser, so the unpacking of the hoisted weight
@@ -177,7 +186,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
 #pragma unroll
       for (int k = 0; k < ITEMS; ++k) {
         const int v = threadIdx.x + k * THREADS;
-        if (v < nvec) {
+        if (in_row(v)) {
           float fw[VEC];
           float f[VEC];
           C::unpack(rov[k], f);
@@ -223,7 +232,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
 #pragma unroll
       for (int k = 0; k < ITEMS; ++k) {
         const int v = threadIdx.x + k * THREADS;
-        if (v < nvec) {
+        if (in_row(v)) {
           uint32_t wq[VEC / 4];
           float f[VEC];
           if constexpr (kPackY) {
@@ -381,12 +390,20 @@ int32_t launch_rmsnorm(const void* x, const void* res, const void* w, void* y, u
     // 126.9 against 134.6 us at 12288 columns, 286.1 against 301.5 at 24576;
     // fp16 172.8 against 184.9 at 16384), static from 3072 (273.3 against
     // 297.7 at 24576). Plain RMSNorm rows lose 3-6 % on such a grid.
-    constexpr auto kernel = rmsnorm_resident<C, S::kThreads, S::kItems, MODE, FMT>;
     constexpr int kCap = S::kThreads * S::kItems;
     constexpr bool kLoop = (MODE == 1 && kCap >= 1536) || (MODE == 2 && kCap >= 3072);
-    const int64_t resident = kLoop ? resident_groups<kernel>(S::kThreads) : 0;
-    const unsigned grid = resident > 0 && resident < (int64_t)g ? (unsigned)resident : g;
-    kernel<<<grid, S::kThreads, 0, st>>>(x, res, w, y, yq, scale, ro, rows, cols, eps, static_scale);
+    auto go = [&](auto full) {
+      constexpr auto kernel = rmsnorm_resident<C, S::kThreads, S::kItems, MODE, FMT, decltype(full)::value>;
+      const int64_t resident = kLoop ? resident_groups<kernel>(S::kThreads) : 0;
+      const unsigned grid = resident > 0 && resident < (int64_t)g ? (unsigned)resident : g;
+      kernel<<<grid, S::kThreads, 0, st>>>(x, res, w, y, yq, scale, ro, rows, cols, eps, static_scale);
+    };
+    // A row that fills the shape exactly in whole 512-addend regions takes
+    // the compile-time-planned kernel (no per-vector bounds checks, no tail).
+    if constexpr (C::VEC == 8 && (kCap * 8) % kRegionAddends == 0) {
+      if (nvec == kCap) return go(std::true_type{});
+    }
+    go(std::false_type{});
   };
   // 16-byte rows (f16 / bf16): the shapes come from a sweep over every
   // THREADS in 64..1024 (step 64) x ITEMS in 1..4 holding the row, on MI355X
