@@ -186,21 +186,37 @@ template <int NB>
 __device__ inline float aten_finish_full(const float* bs, int lane) {
   float q = 0.0f;
   if (lane < kFoldLanes) {
-    float f[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) f[b] = bs[b * kFoldLanes + lane];
     if constexpr (NB <= 16) {
+      float f[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) f[b] = bs[b * kFoldLanes + lane];
       q = f[0];
 #pragma unroll
       for (int b = 1; b < NB; ++b) q = q + f[b];
     } else {
-      // FoldCascade's operations with the block indices unrolled.
-      FoldCascade cs;
+      // FoldCascade's operations, a group of 16 blocks (acc1 from zero, then
+      // promoted into acc2) at a time, so at most 16 folds are held at once.
+      float a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll 1
+      for (int j = 0; j < NB / 16; ++j) {
+        float f[16];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) cs.add(f[b], b, 4);
-      q = cs.a1;
-      if constexpr (NB >= 16) q = q + cs.a2;
-      if constexpr (NB >= 256) q = q + cs.a3;
+        for (int i = 0; i < 16; ++i) f[i] = bs[(16 * j + i) * kFoldLanes + lane];
+        a1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a1 = a1 + f[i];
+        a2 = a2 + a1;
+        a1 = 0.0f;
+        if ((16 * (j + 1)) % 256 == 0) {
+          a3 = a3 + a2;
+          a2 = 0.0f;
+        }
+      }
+#pragma unroll
+      for (int b = NB / 16 * 16; b < NB; ++b) a1 = a1 + bs[b * kFoldLanes + lane];
+      q = a1;
+      q = q + a2;
+      if constexpr (NB >= 256) q = q + a3;
     }
   }
   const float q1 = swizzle_xor<8>(q), q2 = swizzle_xor<16>(q), q3 = swizzle_xor<24>(q);

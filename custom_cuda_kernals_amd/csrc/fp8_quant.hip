@@ -567,66 +567,52 @@ int32_t launch_token(const void* x, uint8_t* q, float* scale, int64_t m, int64_t
 }
 
 // ---------------------------------------------------------------------------
-// Tensor granularity with no memory from the caller beyond the input and the
-// outputs (no counterpart in the reference; for callers that cannot allocate:
-// code under HIP graph capture, serving loops). Its state lives in `scratch`,
-// a file-scope device array of kScratchWords words (6.5 KiB), one per GPU,
-// held until the process ends. Every call on a device shares that device's
-// array: calls that overlap on one GPU (on different streams) race.
+// Tensor granularity in one read of x (fp8_tensor_onepass). Each workgroup of
+// 1024 threads keeps its share of x in registers (U 16-byte vectors per
+// thread) and takes its max |x|. Workgroup 0 is the reducer: every other
+// workgroup b stores its maximum into slot b and then waits for the scale;
+// workgroup 0 waits until every slot is filled, reduces them with its own
+// maximum, does the caller's atomicMax (if any), and publishes the scale in
+// the caller's `scale` word. Every workgroup then converts what it holds.
 //
-// Inputs that fit in the registers of a grid that is resident at once take
-// fp8_tensor_onepass: x is read from HBM once and the op is one launch. The
-// others take the two-pass form above, with the partial maxima in the slots
-// and every cast workgroup reducing them itself (each call writes every slot
-// it reads, so nothing needs clearing).
+// All of the exchange lives in memory the call owns: the slots are words
+// 1 .. g-1 of the codes buffer, inside workgroup 0's own share of the codes
+// (the launcher checks 4 g <= that share), and the result is the scale
+// output. fp8_onepass_init (one small launch on the same stream, before the
+// one-pass launch, for grids of two or more) marks the slots empty
+// (kSlotEmpty, never the bits of a maximum |x|: those have the sign bit
+// clear) and the scale unpublished (kScaleEmpty, a signalling NaN, never a
+// computed scale: arithmetic on a NaN quiets it). Nothing persists between
+// calls, so calls on different streams may overlap freely, and graph replays
+// need nothing cleared. Each slot is written once, before its workgroup
+// waits, so once workgroup 0 has seen every slot no slot is written again
+// and its codes may land on them.
 //
-// fp8_tensor_onepass: each workgroup keeps its share of x in registers,
-// stores its max |x| bits into its slot, and arrives at the counter of its
-// group (workgroup b is in group b % 8; workgroups are dealt to the 8 XCDs
-// round-robin, so a group is one XCD's share). The last arrival of a group
-// resets that counter and arrives at the top counter; the last arrival there
-// resets it, reduces the slots and publishes {generation + 1, amax bits} in
-// the result word. Every other workgroup polls the result word until its
-// generation moves past the one it read before arriving, then converts what
-// it holds. Counters return to zero in every call and the generation only
-// moves forward, so no call needs memory cleared.
+// Every shared word is written and read only by agent-scope atomics, which
+// gfx950 performs beyond the per-XCD L2s, and a slot's store completes
+// before its workgroup starts to wait.
 //
-// Every word shared between workgroups is read and written only by
-// agent-scope atomics, which gfx950 performs beyond the per-XCD L2s, and a
-// workgroup waits for its slot store to complete before it arrives. That wait
-// is the ordering an agent-scope release gives atomic data; the release's L2
-// writeback and the acquire's L2 invalidation serve only non-atomic data and
-// are left out (6.8-6.9 vs 8.5-9.9 us per launch for the exchange at
-// [2048, 4096] bf16 on MI355X).
-//
-// Waiting needs the whole grid resident at once: the launcher sizes the grid
-// to the occupancy the runtime reports for the device. A workgroup whose wait
-// still runs past the poll limit (other work holding CUs) reads all of x and
-// takes the maximum itself, so the result never depends on residency.
+// Waiting needs the grid resident at once: the launcher sizes it to the
+// occupancy the runtime reports for the device. A workgroup other than 0
+// whose wait runs past its poll limit (other work holding CUs) reads all of
+// x and takes the maximum itself (and the caller's int32), then converts:
+// the same scale, so the result never depends on residency. Those
+// workgroups leave, so the ones not yet running get CUs and fill their
+// slots: workgroup 0's wait, the only one without a limit, always ends.
 // ---------------------------------------------------------------------------
-constexpr int kOnePassThreads = 1024, kOnePassMaxGroups = 1024;
-constexpr int kLineWords = 64;  // counters and the result word each own a 256-byte line
-constexpr int kGroupCounter = kOnePassMaxGroups;                  // + group * kLineWords, group < 8
-constexpr int kTopCounter = kGroupCounter + 8 * kLineWords;
-constexpr int kResultWord = kTopCounter + kLineWords;             // 64-bit {generation, amax bits}
-constexpr int kScratchWords = kResultWord + kLineWords;
-static_assert(kOnePassMaxGroups >= kPartialMaxGroups, "the two-pass form's partial maxima use the same slots");
-static_assert(kResultWord % 2 == 0, "the result word is 8-byte aligned");
-
-static __device__ __align__(256) uint32_t scratch[kScratchWords];
+constexpr int kOnePassThreads = 1024;
+constexpr uint32_t kSlotEmpty = 0xffffffffu;
+constexpr uint32_t kScaleEmpty = 0x7f800001u;
+// Polls (about 1 us each: a short sleep and a load from beyond the L2) a
+// waiting workgroup makes before it reads all of x itself; the exchange
+// itself takes about 3 us.
+constexpr int kDefaultPollLimit = 2048;
 
 __device__ inline uint32_t agent_load(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ inline uint64_t agent_load(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <class T>
-__device__ inline void agent_store(T* p, T v) {
+__device__ inline void agent_store(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline uint32_t agent_add(uint32_t* p, uint32_t v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Wait until this thread's memory operations have completed (s_waitcnt with
 // every counter at zero); the compiler moves no memory access across it.
@@ -636,23 +622,38 @@ __device__ inline void wait_memory_ops() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// U 16-byte vectors per thread; requires 16-byte aligned x, VEC-aligned q,
-// total % VEC == 0 and gridDim.x <= kOnePassMaxGroups, all resident at once.
-// At most 64 VGPRs (8 waves per SIMD), so a CU holds two workgroups at every
-// U: U = 8 spills 20 bytes per lane, and at [8192, 4096] bf16 takes 21.6 us
-// against 28.8 us for the two-pass form it replaces at that size.
-template <class C, int FMT, int U>
-__global__ __launch_bounds__(kOnePassThreads, 8) void fp8_tensor_onepass(const void* __restrict__ x,
-                                                                      uint8_t* __restrict__ q,
-                                                                      float* __restrict__ scale_out, int64_t nvec,
-                                                                      uint32_t* __restrict__ sync, int poll_limit) {
+__global__ __launch_bounds__(256) void fp8_onepass_init(uint32_t* __restrict__ slots, int groups,
+                                                        float* __restrict__ scale) {
+  for (int i = 1 + (int)threadIdx.x; i < groups; i += 256) agent_store(slots + i, kSlotEmpty);
+  if (threadIdx.x == 0) agent_store(reinterpret_cast<uint32_t*>(scale), kScaleEmpty);
+}
+
+// The scale of amax bits m together with the caller's int32 (if any; its
+// value before or after the reducer's atomicMax gives the same maximum).
+template <int FMT>
+__device__ inline float tensor_scale(uint32_t m, const int32_t* amax_scratch) {
+  if (amax_scratch != nullptr) {
+    const int32_t seen = (int32_t)agent_load(reinterpret_cast<const uint32_t*>(amax_scratch));
+    m = (uint32_t)max(seen, (int32_t)m);
+  }
+  return scale_from_amax<FMT>(bits_f32(m));
+}
+
+// U 16-byte vectors per thread and at least WPE waves per SIMD (the register
+// budget: 512 / WPE VGPRs, no spills); requires 16-byte aligned x,
+// VEC-aligned q, total % VEC == 0, 4 * gridDim.x <= 1024 * U * VEC (the slots
+// fit in workgroup 0's codes) and fp8_onepass_init on the same stream first
+// when gridDim.x > 1.
+template <class C, int FMT, int U, int WPE>
+__global__ __launch_bounds__(kOnePassThreads, WPE) void fp8_tensor_onepass(
+    const void* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ scale_out,
+    int32_t* __restrict__ amax_scratch, int64_t nvec, int poll_limit) {
   constexpr int T = kOnePassThreads, NW = T / 64;
   __shared__ uint32_t lds[2 * NW];
-  __shared__ uint32_t last_s, late_s, amax_s;
+  __shared__ uint32_t scale_s, late_s;
   const u32x4* xv = static_cast<const u32x4*>(x);
-  uint64_t* result = reinterpret_cast<uint64_t*>(sync + kResultWord);
-  uint32_t gen = 0;
-  if (threadIdx.x == 0) gen = (uint32_t)(agent_load(result) >> 32);
+  uint32_t* slots = reinterpret_cast<uint32_t*>(q);
+  uint32_t* scale_bits = reinterpret_cast<uint32_t*>(scale_out);
   const int64_t b0 = (int64_t)blockIdx.x * T * U + threadIdx.x;
   u32x4 raw[U];
 #pragma unroll
@@ -664,51 +665,52 @@ __global__ __launch_bounds__(kOnePassThreads, 8) void fp8_tensor_onepass(const v
   for (int k = 0; k < U; ++k) {
     if (b0 + k * T < nvec) acc = C::absmax_vec(raw[k], acc);
   }
-  acc = block_allreduce<NW>(acc, typename AmaxOp<C>::type{}, lds, 0);
-  if (threadIdx.x == 0) {
-    agent_store(sync + blockIdx.x, f32_bits(C::absmax_to_float(acc)));
-    wait_memory_ops();
-    const unsigned g = gridDim.x, c = blockIdx.x % 8;
-    uint32_t* group = sync + kGroupCounter + c * kLineWords;
-    bool last = agent_add(group, 1u) == (g - c + 7) / 8 - 1;
-    if (last) {
-      agent_store(group, 0u);
-      last = agent_add(sync + kTopCounter, 1u) == min(g, 8u) - 1;
-      if (last) agent_store(sync + kTopCounter, 0u);
+  const uint32_t mine =
+      f32_bits(C::absmax_to_float(block_allreduce<NW>(acc, typename AmaxOp<C>::type{}, lds, 0)));
+  if (blockIdx.x == 0) {
+    uint32_t m = mine;
+    for (unsigned i = 1 + threadIdx.x; i < gridDim.x; i += T) {
+      uint32_t v = agent_load(slots + i);
+      while (v == kSlotEmpty) {
+        __builtin_amdgcn_s_sleep(1);
+        v = agent_load(slots + i);
+      }
+      m = max(m, v);
     }
-    last_s = last;
-  }
-  __syncthreads();
-  uint32_t amax_bits;
-  if (last_s) {
-    uint32_t m = 0;
-    for (unsigned i = threadIdx.x; i < gridDim.x; i += T) m = max(m, agent_load(sync + i));
-    amax_bits = block_allreduce<NW>(m, MaxU32{}, lds, 1);
-    if (threadIdx.x == 0) agent_store(result, ((uint64_t)(gen + 1) << 32) | amax_bits);
+    m = block_allreduce<NW>(m, MaxU32{}, lds, 1);
+    if (threadIdx.x == 0) {
+      if (amax_scratch != nullptr) m = (uint32_t)max(atomicMax(amax_scratch, (int32_t)m), (int32_t)m);
+      const uint32_t sb = f32_bits(scale_from_amax<FMT>(bits_f32(m)));
+      agent_store(scale_bits, sb);
+      scale_s = sb;
+    }
   } else {
     if (threadIdx.x == 0) {
-      uint64_t w = agent_load(result);
-      for (int i = 0; (uint32_t)(w >> 32) == gen && i < poll_limit; ++i) {
+      agent_store(slots + blockIdx.x, mine);
+      wait_memory_ops();
+      uint32_t v = agent_load(scale_bits);
+      for (int i = 0; v == kScaleEmpty && i < poll_limit; ++i) {
         __builtin_amdgcn_s_sleep(2);
-        w = agent_load(result);
+        v = agent_load(scale_bits);
       }
-      amax_s = (uint32_t)w;
-      late_s = (uint32_t)(w >> 32) == gen;
+      scale_s = v;
+      late_s = v == kScaleEmpty;
     }
     __syncthreads();
-    amax_bits = amax_s;
     if (late_s) {
       // The wait ran past its limit: the maximum over all of x, read by this workgroup.
       uint32_t a = 0;
       for (int64_t v = threadIdx.x; v < nvec; v += T) a = C::absmax_vec(ld_stream(xv + v), a);
-      amax_bits = f32_bits(C::absmax_to_float(block_allreduce<NW>(a, typename AmaxOp<C>::type{}, lds, 1)));
+      const uint32_t m = f32_bits(C::absmax_to_float(block_allreduce<NW>(a, typename AmaxOp<C>::type{}, lds, 1)));
+      if (threadIdx.x == 0) scale_s = f32_bits(tensor_scale<FMT>(m, amax_scratch));
     }
   }
-  const float amax_t = bits_f32(amax_bits);
-  const float s = scale_from_amax<FMT>(amax_t);
-  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
+  __syncthreads();
+  const float s = bits_f32(scale_s);
   const float r = 1.0f / s;
-  const bool fast = fast_path_ok<FMT>(s, r, amax_t);
+  // s >= amax / FP8_MAX keeps |x| * (1/s) within the conversion's verified
+  // range, so only s and 1/s need checking.
+  const bool fast = fast_path_ok<FMT>(s, r, 0.0f);
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     const int64_t v = b0 + k * T;
@@ -717,10 +719,83 @@ __global__ __launch_bounds__(kOnePassThreads, 8) void fp8_tensor_onepass(const v
 }
 
 constexpr int kMaxDevices = 64;
-constexpr int kDefaultPollLimit = 1 << 16;  // polls of about 1 us each before a workgroup reads x itself
+std::mutex onepass_mu;
+std::atomic<int> poll_limit{kDefaultPollLimit};
+
+// Workgroups of fp8_tensor_onepass<C, FMT, U, WPE> the current device holds
+// at once (occupancy per CU x CUs; 0 if unknown).
+template <class C, int FMT, int U, int WPE>
+int onepass_groups() {
+  static int groups[kMaxDevices] = {};  // per instantiation; -1 = the query failed
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  std::lock_guard<std::mutex> lock(onepass_mu);
+  if (groups[dev] == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fp8_tensor_onepass<C, FMT, U, WPE>, kOnePassThreads,
+                                                     0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      groups[dev] = -1;
+    } else {
+      groups[dev] = per_cu * cus > 0 ? per_cu * cus : -1;
+    }
+  }
+  return std::max(groups[dev], 0);
+}
+
+// Inputs from this many vectors up take the one-pass form when it fits;
+// below it (and above one workgroup's worth) the init launch and the
+// exchange cost more than the second read of x saves. Measured on MI355X,
+// bf16 rows of 4096, graph-replayed, one-pass against the two-pass forms
+// (reference ABI with the caller's zero-fill / no amax word): [1024, 4096]
+// 9.73 / 7.78 against 9.32 / 7.50 us; [2048, 4096] (2^20 vectors) 11.54 /
+// 9.58 against 11.67 / 9.92; [4096, 4096] 14.83 / 12.92 against 18.52 /
+// 16.67; [8192, 4096] 24.04 / 22.12 against 29.66 / 27.76.
+constexpr int64_t kOnePassMinVecs = int64_t(1) << 20;
+constexpr int64_t kOnePassSoloVecs = (int64_t)kOnePassThreads * 2;  // one workgroup: no exchange
+
+// Launches the one-pass form where it pays: inputs one workgroup holds
+// (no exchange and no init launch: the fewest vectors per thread that
+// hold x), and inputs of at least kOnePassMinVecs vectors whose grid the
+// device holds at once, with the fewest vectors per thread that allow it:
+// U = 1, 2 or 4 at two workgroups per CU (64 VGPRs), then U = 16 at one
+// (128 VGPRs), after fp8_onepass_init. False otherwise.
+template <class C, int FMT>
+bool launch_onepass(const void* x, uint8_t* q, float* scale, int32_t* amax_scratch, int64_t nvec,
+                    hipStream_t st) {
+  if (nvec > kOnePassSoloVecs && nvec < kOnePassMinVecs) return false;
+  const int polls = poll_limit.load(std::memory_order_relaxed);
+  auto attempt = [&](auto u, auto wpe) {
+    constexpr int U = decltype(u)::value, WPE = decltype(wpe)::value;
+    constexpr int64_t per_group = (int64_t)kOnePassThreads * U;
+    const int64_t g = (nvec + per_group - 1) / per_group;
+    if (nvec <= kOnePassSoloVecs ? g > 1 : (g > onepass_groups<C, FMT, U, WPE>() || 4 * g > per_group * C::VEC)) {
+      return false;
+    }
+    if (g > 1) {
+      fp8_onepass_init<<<1, 256, 0, st>>>(reinterpret_cast<uint32_t*>(q), (int)g, scale);
+    }
+    fp8_tensor_onepass<C, FMT, U, WPE><<<(unsigned)g, kOnePassThreads, 0, st>>>(x, q, scale, amax_scratch, nvec,
+                                                                              polls);
+    return true;
+  };
+  return attempt(IntC<1>{}, IntC<8>{}) || attempt(IntC<2>{}, IntC<8>{}) || attempt(IntC<4>{}, IntC<8>{}) ||
+         attempt(IntC<16>{}, IntC<4>{});
+}
+
+// The no-allocation entry point's two-pass form (inputs beyond the one-pass
+// capacity, or unaligned) keeps its partial maxima in `scratch`, a file-scope
+// device array of kPartialMaxGroups words (2 KiB), one per GPU, held until
+// the process ends. Each call writes every slot it reads, so nothing needs
+// clearing; calls of this form that overlap on one GPU race on the array.
+constexpr int kScratchWords = kPartialMaxGroups;
+static __device__ __align__(256) uint32_t scratch[kScratchWords];
 std::mutex scratch_mu;
 uint32_t* scratch_dev[kMaxDevices] = {};
-std::atomic<int> poll_limit{kDefaultPollLimit};
 
 // The current device's address of `scratch`, looked up once per device. The
 // host-side name of the array is only a handle for the runtime: kernels are
@@ -739,47 +814,6 @@ int32_t scratch_address(uint32_t** out) {
   }
   *out = scratch_dev[dev];
   return (int32_t)hipSuccess;
-}
-
-// Workgroups of fp8_tensor_onepass<C, FMT, U> the current device holds at
-// once (occupancy per CU x CUs, at most kOnePassMaxGroups; 0 if unknown).
-template <class C, int FMT, int U>
-int onepass_groups() {
-  static int groups[kMaxDevices] = {};  // per instantiation; -1 = the query failed
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    (void)hipGetLastError();
-    return 0;
-  }
-  std::lock_guard<std::mutex> lock(scratch_mu);
-  if (groups[dev] == 0) {
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fp8_tensor_onepass<C, FMT, U>, kOnePassThreads, 0) !=
-            hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-      (void)hipGetLastError();
-      groups[dev] = -1;
-    } else {
-      groups[dev] = per_cu * cus > 0 ? std::min(per_cu * cus, kOnePassMaxGroups) : -1;
-    }
-  }
-  return std::max(groups[dev], 0);
-}
-
-// Launches fp8_tensor_onepass with the fewest vectors per thread (U = 1, 2, 4
-// or 8) whose grid the device holds at once; false if none does.
-template <class C, int FMT>
-bool launch_onepass(const void* x, uint8_t* q, float* scale, int64_t nvec, uint32_t* sync, hipStream_t st) {
-  const int polls = poll_limit.load(std::memory_order_relaxed);
-  auto attempt = [&](auto u) {
-    constexpr int U = decltype(u)::value;
-    const int64_t per_group = (int64_t)kOnePassThreads * U;
-    const int64_t g = (nvec + per_group - 1) / per_group;
-    if (g > onepass_groups<C, FMT, U>()) return false;
-    fp8_tensor_onepass<C, FMT, U><<<(unsigned)g, kOnePassThreads, 0, st>>>(x, q, scale, nvec, sync, polls);
-    return true;
-  };
-  return attempt(IntC<1>{}) || attempt(IntC<2>{}) || attempt(IntC<4>{}) || attempt(IntC<8>{});
 }
 
 }  // namespace
@@ -814,13 +848,19 @@ extern "C" int32_t launch_fp8_quant_block_fwd(const void* x, uint8_t* x_fp8, flo
       constexpr int FMT = decltype(f)::value;
       const bool vec_ok = (n % C::VEC == 0) && host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
       const bool rsrc_ok = (int64_t)kTile * n * C::kBytes <= 0x7fffffff;
-      if (vec_ok && rsrc_ok && nrb * ncb >= kBlockPairMinTiles) {
-        // Two tiles side by side per 1024-thread workgroup: 128.0 vs 131.0 us at
-        // [32768, 8192] bf16, 254.5 vs 265.1 us at [65536, 8192]; no gain below
-        // 16384 tiles (65.7 vs 66.3 us at [16384, 8192] for one tile).
-        const dim3 grid2((unsigned)((ncb + 1) / 2), (unsigned)nrb);
-        fp8_block_resident<C, FMT, 512, true, 2><<<grid2, 1024, 0, st>>>(x, x_fp8, scale, m, n);
-      } else if (vec_ok && rsrc_ok && nrb * ncb <= kBlockSplitMaxTiles) {
+      if constexpr (C::VEC == 8) {
+        if (vec_ok && rsrc_ok && nrb * ncb >= kBlockPairMinTiles) {
+          // Two tiles side by side per 1024-thread workgroup: 128.0 vs 131.0 us
+          // at [32768, 8192] bf16, 254.5 vs 265.1 us at [65536, 8192]; no gain
+          // below 16384 tiles (65.7 vs 66.3 us at [16384, 8192] for one tile).
+          // fp32 tiles (8 vectors per thread) do not fit two to a workgroup's
+          // registers and keep one.
+          const dim3 grid2((unsigned)((ncb + 1) / 2), (unsigned)nrb);
+          fp8_block_resident<C, FMT, 512, true, 2><<<grid2, 1024, 0, st>>>(x, x_fp8, scale, m, n);
+          return launch_status();
+        }
+      }
+      if (vec_ok && rsrc_ok && nrb * ncb <= kBlockSplitMaxTiles) {
         // All tiles resident at once: issuing every load of a tile before
         // its max measured 6.44 vs 6.56 us at [2048, 4096] bf16 on MI355X,
         // but 35.9 vs 35.1 us at [16384, 4096], where tiles run in rounds.
@@ -849,6 +889,10 @@ extern "C" int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, fl
       constexpr int FMT = decltype(f)::value;
       const bool vec_ok = host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
       const int64_t nvec = total / C::VEC;
+      // One read of x where the registers of a resident grid hold it.
+      if (vec_ok && total % C::VEC == 0 && launch_onepass<C, FMT>(x, x_fp8, scale, amax_scratch, nvec, st)) {
+        return launch_status();
+      }
       const unsigned gp = vec_ok ? flat_grid(nvec, kPartialThreads * kPartialUnroll, kPartialMaxGroups)
                                  : flat_grid(total, kPartialThreads * 16, kPartialMaxGroups);
       if (vec_ok) {
@@ -931,7 +975,7 @@ extern "C" int32_t launch_fp8_quant_tensor_noalloc_fwd(const void* x, uint8_t* x
       const int32_t rc = scratch_address(&scr);
       if (rc != 0) return rc;
       const bool vec_ok = host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
-      if (vec_ok && total % C::VEC == 0 && launch_onepass<C, FMT>(x, x_fp8, scale, total / C::VEC, scr, st)) {
+      if (vec_ok && total % C::VEC == 0 && launch_onepass<C, FMT>(x, x_fp8, scale, nullptr, total / C::VEC, st)) {
         return launch_status();
       }
       if (vec_ok) {

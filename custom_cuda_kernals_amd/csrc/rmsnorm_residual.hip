@@ -179,7 +179,8 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
       // 137.4, 256 x 3 at 5120 53.4 vs 54.1); static 256 x 3 at 5120 54.1 vs
       // 52.5, 512 x 3 at 12288 124.1 vs 122.1 (but 512 x 4 at 16384 163.5 vs
       // 166.8).
-      constexpr bool kPackY = (MODE == 1 && ITEMS >= 4) || (MODE == 2 && ITEMS == 3);
+      constexpr bool kPackY =
+          (MODE == 1 && ITEMS >= 4) || (MODE == 2 && (ITEMS == 3 || (ITEMS == 4 && THREADS == 1024)));
       float yv[kPackY ? 1 : ITEMS][VEC];
       u32x4 yp[kPackY ? ITEMS : 1];
       float amax = 0.0f;

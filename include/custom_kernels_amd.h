@@ -74,9 +74,16 @@ int32_t launch_fp8_quant_block_fwd(const void* x, uint8_t* x_fp8, float* scale, 
  * int32 [1], caller-zeroed before every call, left holding the bits of
  * max |x| (atomically max-ed in, as in the reference; a nonzero initial value
  * takes part in the maximum and so in the scale). amax_scratch may be NULL
- * (an addition): then no amax word is written. Between the call's kernels,
- * x_fp8 also holds per-workgroup maxima, which the cast overwrites.
- * Replaces reference csrc/includes/fp8_quant.h:51-60. */
+ * (an addition): then no amax word is written. While the call runs, x_fp8
+ * and scale also hold its exchange of per-workgroup maxima, which the codes
+ * and the final scale overwrite; the call keeps no other state, so calls on
+ * different streams may overlap. Inputs of 2^20 or more 16-byte vectors that
+ * fit in the registers of a grid the GPU holds at once (up to 64 MiB of x on
+ * MI355X) are read from HBM once. Where such a grid is not resident at once
+ * (other work holding CUs), its waiting workgroups give up after about 2 ms
+ * and each reads all of x itself: slower (one more read of x per such
+ * workgroup, at most 511), never wrong. Replaces reference
+ * csrc/includes/fp8_quant.h:51-60. */
 int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, float* scale,
                                     int32_t* amax_scratch, int64_t m, int64_t n, int32_t dtype,
                                     int32_t fp8_format, void* stream);
@@ -93,13 +100,15 @@ int32_t launch_fp8_quant_token_fwd(const void* x, uint8_t* x_fp8, float* scale, 
 /* As launch_fp8_quant_tensor_fwd (same codes and scale), with no caller
  * memory beyond x, x_fp8 and scale: no counterpart in the reference. For
  * callers that cannot allocate (code under HIP graph capture, serving loops,
- * harnesses that forbid hipMalloc); it calls no allocating routine. Its
- * per-workgroup maxima and arrival counters live in a 6656-byte device array
- * owned by the library, one per GPU, held until the process ends; any m * n
- * that fits int64 works (else hipErrorInvalidValue, before any device call).
- * An input that fits in the registers of a grid the GPU holds at once is
- * read once, in one launch. Every call on a GPU shares that GPU's array, so
- * calls that overlap on one GPU race. */
+ * harnesses that forbid hipMalloc); it calls no allocating routine, and none
+ * of its kernels needs scratch memory. Inputs that take the one-pass form
+ * (as launch_fp8_quant_tensor_fwd, with x_fp8 and scale holding the exchange)
+ * keep no state between calls. The others take a two-pass form whose
+ * per-workgroup maxima live in a 2048-byte device array owned by the
+ * library, one per GPU, held until the process ends: such calls that overlap
+ * on one GPU race on it (each call rewrites every word it reads, so later
+ * calls are unaffected). Any m * n that fits int64 works (else
+ * hipErrorInvalidValue, before any device call). */
 int32_t launch_fp8_quant_tensor_noalloc_fwd(const void* x, uint8_t* x_fp8, float* scale, int64_t m,
                                             int64_t n, int32_t dtype, int32_t fp8_format, void* stream);
 
@@ -209,10 +218,11 @@ int32_t cck_scale_selftest(uint64_t start, uint64_t count, int32_t fp8_format,
  * layout. */
 int32_t cck_silu_table_selftest(unsigned long long* counters, void* stream);
 
-/* Test hook (no reference counterpart): sets the number of polls a
- * workgroup of the one-pass launch_fp8_quant_tensor_noalloc_fwd makes for the
- * device-wide maximum before it reads all of x and takes the maximum itself
- * (default 65536); polls < 0 only queries. Returns the previous value. Takes
+/* Test hook (no reference counterpart): sets the number of polls (about
+ * 1 us each) a waiting workgroup of the one-pass per-tensor FP8 form
+ * (launch_fp8_quant_tensor_fwd and launch_fp8_quant_tensor_noalloc_fwd) makes
+ * for the scale before it reads all of x and takes the maximum itself
+ * (default 2048); polls < 0 only queries. Returns the previous value. Takes
  * effect for later launches. */
 int32_t cck_fp8_tensor_noalloc_poll_limit(int32_t polls);
 

@@ -336,7 +336,7 @@ def test_noalloc_poll_limit_hook_is_host_state():
     device call), default 65536, returned on change and restorable."""
     lib = _cck.load()
     prev = lib.cck_fp8_tensor_noalloc_poll_limit(-1)
-    assert prev == 65536
+    assert prev == 2048
     assert lib.cck_fp8_tensor_noalloc_poll_limit(17) == prev
     assert lib.cck_fp8_tensor_noalloc_poll_limit(-1) == 17
     assert lib.cck_fp8_tensor_noalloc_poll_limit(prev) == 17

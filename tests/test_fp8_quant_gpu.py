@@ -142,16 +142,21 @@ def test_rejects_bad_format_and_granularity():
         fp8_quant(x, "e4m3", "block", scale=0.1)
 
 
-# ---- Tensor granularity: the three-step maximum (per-workgroup partial maxima
-# in the codes buffer, one finishing atomicMax into the caller's int32, then
+# ---- Tensor granularity: the one-pass exchange (workgroup maxima in slots in
+# workgroup 0's share of the codes, the scale published in the scale word) and
+# the two-pass forms (partial maxima in the codes buffer, a finishing
+# atomicMax into the caller's int32 or slot arrays in the cast chunks, then
 # the cast), exercised through the C ABI where the Python API cannot reach.
 
 @pytest.mark.parametrize("where", ["first", "middle", "last"])
-@pytest.mark.parametrize("shape", [(1, 1), (1, 3), (2, 3), (3, 1001), (4099, 4097)], ids=lambda s: f"{s[0]}x{s[1]}")
+@pytest.mark.parametrize("shape", [(1, 1), (1, 3), (2, 3), (3, 1001), (4099, 4097), (2048, 4096), (8192, 4096)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
 def test_tensor_amax_found_anywhere(shape, where):
     """The largest |x| at the first, middle or last element: sizes below the
-    partial-slot minimum, a scalar tail after the 16-byte vectors, and a grid
-    of 512 partial workgroups that each stride over several vectors."""
+    partial-slot minimum, a scalar tail after the 16-byte vectors, a grid of
+    512 partial workgroups that each stride over several vectors, and one-pass
+    grids (the maximum in workgroup 0's own share, in the middle workgroup's,
+    in the last one's)."""
     x = inputs.randn(shape, torch.bfloat16, seed=shape[0] * 31 + shape[1])
     flat = x.view(-1)
     idx = {"first": 0, "middle": flat.numel() // 2, "last": flat.numel() - 1}[where]
@@ -174,16 +179,20 @@ def _tensor_abi(x_dev: torch.Tensor, q: torch.Tensor, scratch: torch.Tensor | No
     return scale
 
 
-# (shape, what it reaches for bf16 / fp16; fp32 alike unless noted)
+# (shape, what it reaches for bf16 / fp16; fp32 alike unless noted). The
+# one-pass form takes inputs of at most 2048 vectors (one workgroup) and of at
+# least 2^20 vectors up to what a resident grid holds in registers.
 TENSOR_PATHS = [
     ((1024, 4096), "bf16/fp16: slot arrays in every cast chunk, XCD-aligned cast order; fp32: the finishing launch"),
     ((300, 4096), "slot arrays written by 75 partial workgroups (not a multiple of 8), chunks walked last-first"),
-    ((2048, 4096), "the finishing launch, XCD-aligned cast order (config 1)"),
-    ((4099, 4097), "the finishing launch, a scalar tail after the vectors"),
+    ((2048, 4096), "one pass (config 1): 2 vectors per thread over 512 workgroups (fp32: 4)"),
+    ((4096, 4096), "one pass: 4 vectors per thread over 512 workgroups (fp32: 16 over 256)"),
+    ((8192, 4096), "one pass: 16 vectors per thread over 256 workgroups, the register capacity (fp32: two passes)"),
+    ((4099, 4097), "two passes: the finishing launch, a scalar tail after the vectors"),
     ((4, 20482), "last cast chunk too short for a slot array: the finishing launch"),
-    ((5, 2056), "slot arrays: one or two partial workgroups, two or three cast chunks"),
+    ((5, 2056), "one pass in one workgroup, no exchange (fp32: two passes, slot arrays)"),
     ((2, 3), "bf16/fp16: no whole vector, the finishing launch over scalars; fp32: a one-word slot array, a tail"),
-    ((1, 8), "one vector: a slot array in the only chunk"),
+    ((1, 8), "one vector: one pass in one workgroup"),
     ((1, 3), "too small for one slot: the one-workgroup amax"),
 ]
 

@@ -112,13 +112,17 @@ def test_rope_in_place_graph():
     _replay_matches_eager([q, k, cos, sin], [q, k], lambda: native.rope_fwd(q, k, cos, sin, q, k), sets)
 
 
-@pytest.mark.parametrize("gran", ["token", "block", "tensor", "tensor_api", "tensor_api_finish", "static"])
+@pytest.mark.parametrize("gran", ["token", "block", "tensor", "tensor_api", "tensor_api_finish", "tensor_api_onepass",
+                                  "tensor_onepass", "static"])
 def test_fp8_quant_graph(gran):
     """tensor: the reference ABI (its int32 cleared inside the graph); tensor_api:
     no amax word, as the Python API calls it (slot arrays in the cast chunks at
-    this size); tensor_api_finish: the same at 2048 rows (one slot array and
-    the finishing launch)."""
-    m, n = (2048 if gran == "tensor_api_finish" else 256), 4096
+    this size); tensor_api_finish: the same with one slot array and the
+    finishing launch; tensor_api_onepass / tensor_onepass: the one-pass form
+    (its init launch and the exchange in the codes and scale buffers), without
+    and with the amax word."""
+    m, n = {"tensor_api_finish": (4099, 4097), "tensor_api_onepass": (2048, 4096),
+            "tensor_onepass": (4096, 4096)}.get(gran, (256, 4096))
     sets = [[inputs.fp8_token_input(m, n, BF16, seed=s)] for s in range(3)]
     x = sets[0][0].cuda()
     q = torch.empty(m, n, dtype=F8, device="cuda")
@@ -128,7 +132,7 @@ def test_fp8_quant_graph(gran):
     elif gran == "block":
         s = torch.empty(m // 128, n // 128, device="cuda")
         launch, outs = (lambda: native.fp8_quant_block_fwd(x, q, s, "e4m3")), [q, s]
-    elif gran == "tensor":
+    elif gran in ("tensor", "tensor_onepass"):
         s = torch.empty(1, device="cuda")
         amax = torch.zeros(1, dtype=torch.int32, device="cuda")
 

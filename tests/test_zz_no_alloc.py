@@ -1,16 +1,19 @@
-"""launch_fp8_quant_tensor_noalloc_fwd (no caller scratch, library-owned
-device array) against the reference-ABI launch_fp8_quant_tensor_fwd and the
-oracle (baselines/fp8_quant.py:162-178 with one scale for the tensor), bit
-for bit: codes and scale. Two calls in a row, the second on a smaller input,
-so the second call starts from the array as the first left it; plus the
-scalar (unaligned) path, both formats and every input dtype.
+"""launch_fp8_quant_tensor_noalloc_fwd (no caller scratch; a library-owned
+device array for its two-pass form) against the reference-ABI
+launch_fp8_quant_tensor_fwd and the oracle (baselines/fp8_quant.py:162-178
+with one scale for the tensor), bit for bit: codes and scale. Two calls in a
+row, the second on a smaller input, so the second call starts from the array
+as the first left it; plus the scalar (unaligned) path, both formats and
+every input dtype.
 
-Inputs that fit in the registers of a resident grid take the one-pass kernel
-(a device-wide exchange of workgroup maxima through counters and a result
-word in the array); the rest take the two-pass form. Both are covered, with
-calls of either kind queued back to back, and the one-pass kernel's fallback
-(a workgroup whose wait runs out reads all of x itself) is forced from the
-host with a poll limit of zero.
+Inputs of at most one workgroup's worth, and inputs from 2^20 vectors up that
+fit in the registers of a resident grid, take the one-pass kernel (workgroup
+maxima exchanged through slots in the call's own codes buffer and the scale
+published in its scale word); the rest take the two-pass form, with its
+partial maxima in the library's array. Both are covered, with calls of either
+kind queued back to back, and the one-pass kernel's fallback (a workgroup
+whose wait runs out reads all of x itself) is forced from the host with a
+poll limit of zero.
 """
 
 from __future__ import annotations
@@ -111,9 +114,8 @@ def test_unaligned_buffers_take_the_scalar_path():
 
 
 def test_back_to_back_without_synchronising():
-    """Several calls queued on one stream without host synchronisation (each
-    call's last partial workgroup must leave the counter at zero for the
-    next), each checked afterwards against the oracle."""
+    """Several calls queued on one stream without host synchronisation, each
+    checked afterwards against the oracle."""
     xs = [inputs.randn((64 * (i + 1), 4096), torch.bfloat16, seed=20 + i) * (i + 1) for i in range(5)]
     outs = []
     for x in xs:
@@ -128,19 +130,20 @@ def test_back_to_back_without_synchronising():
 
 @pytest.mark.parametrize("shape", [(4096, 8192), (4097, 8192)], ids=lambda s: f"{s[0]}x{s[1]}")
 def test_register_capacity_boundary(shape):
-    """[4096, 8192] bf16 is 8 vectors per thread over 512 workgroups of 1024
-    threads (one pass when the GPU holds 512 at once); one more row is two passes."""
+    """[4096, 8192] bf16 is 16 vectors per thread over 256 workgroups of 1024
+    threads (one pass when the GPU holds 256 at once); one more row is two passes."""
     x = inputs.randn(shape, torch.bfloat16, seed=shape[0])
     x.view(-1)[-5] = 900.0
     _check_pair(x, "e4m3")
 
 
 def test_mixed_sequence_queued_without_synchronising():
-    """One-pass grids of 1, 7, 8, 9, 64 and 512 workgroups (the exchange's
-    group and top counters at every fill), a two-pass input between them and
-    an unaligned one, all queued on one stream before any result is read."""
-    shapes = [(1, 8), (7, 1024 * 8), (8, 1024 * 8), (9, 1024 * 8), (64, 1024 * 8), (2048, 4096), (8193, 8192),
-              (3, 1030), (2048, 4096), (1, 8), (100, 4096)]
+    """One-pass grids of one workgroup (no exchange) and of 256 and 512
+    workgroups, two-pass inputs between them (small ones, which take the
+    library's array, and one beyond the one-pass capacity) and an unaligned
+    one, all queued on one stream before any result is read."""
+    shapes = [(1, 8), (2, 1024 * 8), (7, 1024 * 8), (64, 1024 * 8), (2048, 4096), (8193, 8192), (4096, 8192),
+              (3, 1030), (2048, 4096), (1, 8), (100, 4096), (4096, 4096)]
     xs = [inputs.randn(s, torch.bfloat16, seed=40 + i) * (0.5 + i) for i, s in enumerate(shapes)]
     for i, x in enumerate(xs):
         x.view(-1)[(i * 7919) % x.numel()] = -(3.0 + 50 * i)
@@ -172,9 +175,9 @@ def test_special_values_take_the_exact_path():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
 def test_wait_fallback_reads_x_itself(dtype):
-    """Poll limit 0: every workgroup but the last arrival stops waiting at
-    once and takes the maximum over all of x itself; the results are the same
-    bits, and the exchange state stays consistent for the calls after it."""
+    """Poll limit 0: every workgroup but workgroup 0 (the reducer) stops
+    waiting at once and takes the maximum over all of x itself; the results
+    are the same bits, and the calls after it are unaffected."""
     lib = _lib()
     prev = lib.cck_fp8_tensor_noalloc_poll_limit(0)
     try:
@@ -239,3 +242,29 @@ def test_rejects_size_beyond_int64_before_device_calls():
     assert lib.launch_fp8_quant_tensor_noalloc_fwd(None, None, None, 0, 8, 2, 3, None) == 0
     assert lib.launch_fp8_quant_tensor_noalloc_fwd(None, None, None, 4, 8, 9, 3, None) == 1
     assert lib.launch_fp8_quant_tensor_noalloc_fwd(None, None, None, 4, 8, 2, 7, None) == 1
+
+
+def test_one_pass_calls_overlapping_on_two_streams_then_alone():
+    """One-pass calls queued alternately on two streams without
+    synchronising (their exchanges live in their own outputs, so overlapping
+    calls cannot mix), then a call alone: all bit for bit."""
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    shapes = [(4096, 4096), (2048, 4096), (4096, 8192), (2048, 4096)]
+    xs = [inputs.randn(s, torch.bfloat16, seed=120 + i) * (2 + i) for i, s in enumerate(shapes)]
+    devs = [x.cuda() for x in xs]
+    torch.cuda.synchronize()
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for i, xd in enumerate(devs):
+        with torch.cuda.stream(streams[i % 2]):
+            q = torch.empty(xd.shape, dtype=torch.uint8, device="cuda")
+            outs.append((q, _noalloc(xd, q, "e4m3")))
+    for st in streams:
+        torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    for x, (q, sc) in zip(xs, outs):
+        codes, s_oracle = ofp8.quant_tensor(x.float().numpy(), "e4m3")
+        assert_codes_equal(q, codes)
+        assert_f32_bits_equal(sc, s_oracle)
+    _check_pair(inputs.randn((4096, 4096), torch.bfloat16, seed=129), "e4m3")
