@@ -64,6 +64,9 @@ def _parse():
                    help="layer shapes of the --block decoder block (llama3-70b: hidden 8192, FFN 28672)")
     p.add_argument("--no-ceilings", action="store_true",
                    help="skip the practical-ceiling streams (pure traffic with six config ops' byte patterns)")
+    p.add_argument("--markers", action="store_true",
+                   help="wrap each op's timed graph replay in a ROCTx range named 'timed:<op>', so a "
+                        "rocprofv3 --marker-trace --kernel-trace run can select exactly the timed dispatches")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a 256 MiB device-to-device torch copy, the reference kernel "
                         "for scaling FETCH_SIZE / WRITE_SIZE counters")
@@ -83,6 +86,39 @@ def _c_lib():
     fn.restype = ctypes.c_int32
     fn.argtypes = [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_void_p]
     return lib
+
+
+class _Markers:
+    """ROCTx ranges (rocprofiler-sdk's roctx library) around the timed regions;
+    a no-op when not requested."""
+
+    def __init__(self, enabled):
+        self.lib = None
+        if enabled:
+            import ctypes
+
+            for name in ("librocprofiler-sdk-roctx.so.1", "libroctx64.so.4"):
+                try:
+                    self.lib = ctypes.CDLL(os.path.join("/opt/rocm/lib", name))
+                    break
+                except OSError:
+                    continue
+            if self.lib is None:
+                raise RuntimeError("--markers: no ROCTx library under /opt/rocm/lib")
+            self.lib.roctxRangePushA.argtypes = [ctypes.c_char_p]
+            self.lib.roctxRangePushA.restype = ctypes.c_int
+            self.lib.roctxRangePop.restype = ctypes.c_int
+
+    def push(self, name):
+        if self.lib is not None:
+            self.lib.roctxRangePushA(name.encode())
+
+    def pop(self):
+        if self.lib is not None:
+            self.lib.roctxRangePop()
+
+
+MARKERS = _Markers(False)
 
 
 def _ensure_built():
@@ -324,10 +360,12 @@ def _time_op(torch, op, steps, warmup, use_graph=True, per_call=True):
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    MARKERS.push(f"timed:{op.name}")
     start.record(stream)
     graph.replay()
     end.record(stream)
     torch.cuda.synchronize()
+    MARKERS.pop()
     ms = start.elapsed_time(end)
     us = ms * 1000.0 / steps
     gbps = op.nbytes / (us * 1e-6) / 1e9
@@ -576,6 +614,8 @@ def main():
 
     import torch
 
+    global MARKERS
+    MARKERS = _Markers(args.markers)
     _ensure_built()
     from custom_cuda_kernals_amd._lib import native
 

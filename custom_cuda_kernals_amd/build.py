@@ -80,20 +80,43 @@ def build_library() -> Path:
     return LIB
 
 
-def build_native() -> Path:
-    import pybind11
+def _torch_paths() -> tuple[Path, bool]:
+    """torch's install directory and whether it was built with the C++11 ABI."""
+    import torch
 
-    out = native_ext_path()
-    tmp = out.with_suffix(".tmp")
-    _run([
-        "g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall",
-        f"-I{pybind11.get_include()}",
+    return Path(torch.__file__).resolve().parent, bool(torch._C._GLIBCXX_USE_CXX11_ABI)
+
+
+def native_compile_args(sanitize: bool = False) -> list[str]:
+    """g++ arguments of the binding: torch's headers (for at::Tensor and c10's
+    HIP stream registry; torch's bundled pybind11 comes with them), linked to
+    torch's Python, core and HIP libraries and to the kernel library (C ABI
+    only). `sanitize` adds AddressSanitizer and UndefinedBehaviorSanitizer
+    (host code only; nothing of it is GPU code)."""
+    tdir, cxx11 = _torch_paths()
+    args = [
+        "g++", "-std=c++17", "-shared", "-fPIC", "-Wall",
+        "-D__HIP_PLATFORM_AMD__", f"-D_GLIBCXX_USE_CXX11_ABI={int(cxx11)}",
+        f"-I{tdir / 'include'}", f"-I{tdir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+        "-I/opt/rocm/include",
         f"-I{sysconfig.get_paths()['include']}",
+    ]
+    args += ["-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+             "-fno-sanitize-recover=undefined"] if sanitize else ["-O2"]
+    args += [
         str(CSRC / "native.cpp"),
+        f"-L{tdir / 'lib'}", "-ltorch_python", "-ltorch", "-lc10", "-lc10_hip",
+        f"-Wl,-rpath,{tdir / 'lib'}",
         f"-L{PKG}", "-lcustom_kernels_amd",
         "-Wl,-rpath,$ORIGIN",
-        "-o", str(tmp),
-    ])
+    ]
+    return args
+
+
+def build_native() -> Path:
+    out = native_ext_path()
+    tmp = out.with_suffix(".tmp")
+    _run([*native_compile_args(), "-o", str(tmp)])
     os.replace(tmp, out)
     return out
 

@@ -472,6 +472,8 @@ __global__ __launch_bounds__(VECTOR ? kCastThreads : 256) void fp8_tensor_cast(
   float s;
   if constexpr (STATIC) {
     s = static_scale;
+    // The static scale goes to scale_out[0] when the caller passed a scale word.
+    if (scale_out != nullptr && blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
   } else if constexpr (SRC == kScaleWord) {
     s = scale_out[0];
   } else {
@@ -937,8 +939,8 @@ extern "C" int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, fl
   });
 }
 
-extern "C" int32_t launch_fp8_quant_static_fwd(const void* x, uint8_t* x_fp8, float scale, int64_t m,
-                                               int64_t n, int32_t dtype, int32_t fp8_format,
+extern "C" int32_t launch_fp8_quant_static_fwd(const void* x, uint8_t* x_fp8, float scale, float* scale_out,
+                                               int64_t m, int64_t n, int32_t dtype, int32_t fp8_format,
                                                void* stream) {
   if (m <= 0 || n <= 0) return (int32_t)hipSuccess;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -950,10 +952,10 @@ extern "C" int32_t launch_fp8_quant_static_fwd(const void* x, uint8_t* x_fp8, fl
       const bool vec_ok = host_aligned(x, 16) && host_aligned(x_fp8, C::VEC);
       if (vec_ok) {
         const unsigned g = flat_grid(total / C::VEC, kCastThreads * kCastUnroll, 1 << 20);
-        fp8_tensor_cast<C, FMT, true, true><<<g, kCastThreads, 0, st>>>(x, x_fp8, nullptr, nullptr, scale, total);
+        fp8_tensor_cast<C, FMT, true, true><<<g, kCastThreads, 0, st>>>(x, x_fp8, scale_out, nullptr, scale, total);
       } else {
         const unsigned g = flat_grid(total / C::VEC, 256, 8192);
-        fp8_tensor_cast<C, FMT, true, false><<<g, 256, 0, st>>>(x, x_fp8, nullptr, nullptr, scale, total);
+        fp8_tensor_cast<C, FMT, true, false><<<g, 256, 0, st>>>(x, x_fp8, scale_out, nullptr, scale, total);
       }
       return launch_status();
     });

@@ -107,6 +107,8 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_resident(
   // set-up; later rows (beyond the workgroup cap) load in the loop.
   u32x4 xa[ITEMS], ra[ITEMS];
   if ((int64_t)blockIdx.x < rows) load_row(blockIdx.x, xa, ra);
+  // A static scale goes to scale[0] when the caller passed a scale word.
+  if (MODE == 2 && scale != nullptr && blockIdx.x == 0 && threadIdx.x == 0) scale[0] = static_scale;
   int parity = 0;
   // Rows go to workgroups in blockIdx order, which the dispatcher deals to the
   // 8 XCDs round-robin; measured on MI355X, this beats giving each XCD a
@@ -286,6 +288,7 @@ __global__ __launch_bounds__(256) void rmsnorm_generic(
   const int64_t bvecs = kRegionVecs * nsub;       // vectors per block
   const int64_t nblk = pl.nfull + (pl.has_tail() ? 1 : 0);
   float* a = stage + wave * kRegionAddends;
+  if (MODE == 2 && scale != nullptr && blockIdx.x == 0 && threadIdx.x == 0) scale[0] = static_scale;
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const int64_t base = row * cols;
     FoldCascade cs;
@@ -478,7 +481,7 @@ extern "C" int32_t launch_rmsnorm_residual_fp8_fwd(const void* x, const void* re
         return launch_rmsnorm<C, 1, FMT>(x, residual, weight, nullptr, y_fp8, scale, residual_out, rows,
                                          cols, eps, 0.0f, st);
       }
-      return launch_rmsnorm<C, 2, FMT>(x, residual, weight, nullptr, y_fp8, nullptr, residual_out, rows,
+      return launch_rmsnorm<C, 2, FMT>(x, residual, weight, nullptr, y_fp8, scale, residual_out, rows,
                                        cols, eps, static_scale, st);
     });
   });

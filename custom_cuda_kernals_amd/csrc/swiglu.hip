@@ -78,13 +78,16 @@ __global__ __launch_bounds__(256) void swiglu_scalar(const void* __restrict__ ga
 
 // Static-scale FP8 variant: no row reduction is needed, so it streams like
 // swiglu_flat; each 16-byte vector takes the fast conversion when its own
-// max |y| * (1/s) is inside the fast range, the exact path otherwise.
+// max |y| * (1/s) is inside the fast range, the exact path otherwise. The
+// static kernels also store s into scale_out[0] when given one (the scale
+// tensor the Python API returns), so a static call is one launch.
 template <class C, int FMT, int THREADS, int UNROLL, bool TAB>
 __global__ __launch_bounds__(THREADS) void swiglu_fp8_static_flat(const u32x4* __restrict__ gate,
                                                                  const u32x4* __restrict__ up,
                                                                  uint8_t* __restrict__ yq, float s,
-                                                                 int64_t nvec) {
+                                                                 int64_t nvec, float* __restrict__ scale_out) {
   constexpr int VEC = C::VEC;
+  if (scale_out != nullptr && blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
   __shared__ __attribute__((aligned(16))) float tab[TAB ? SiluTableBF16::kEntries : 1];
   const float r = 1.0f / s;
   const bool scale_ok = fast_path_ok<FMT>(s, r, 0.0f);
@@ -143,7 +146,9 @@ template <class C, int FMT>
 __global__ __launch_bounds__(256) void swiglu_fp8_static_scalar(const void* __restrict__ gate,
                                                                const void* __restrict__ up,
                                                                uint8_t* __restrict__ yq, float s,
-                                                               int64_t begin, int64_t n) {
+                                                               int64_t begin, int64_t n,
+                                                               float* __restrict__ scale_out) {
+  if (scale_out != nullptr && blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
   const float r = 1.0f / s;
   const int64_t stride = (int64_t)gridDim.x * 256;
   for (int64_t i = begin + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
@@ -181,6 +186,8 @@ __global__ __launch_bounds__(THREADS) void swiglu_fp8_resident(
   __shared__ __attribute__((aligned(16))) float tab[TAB ? SiluTableBF16::kEntries : 1];
   const int nvec = (int)(cols / VEC);
   int parity = 0;
+  // A static scale goes to scale[0] when the caller passed a scale word.
+  if (STATIC && scale != nullptr && blockIdx.x == 0 && threadIdx.x == 0) scale[0] = static_scale;
   // Global-pointer row access: for this kernel's 1024 x 2 shape it measured
   // faster than buffer resources on MI355X (96 vs 119 us at [8192, 14336]).
   const uint32_t row_bytes = (uint32_t)(cols * C::kBytes);
@@ -432,7 +439,7 @@ extern "C" int32_t launch_swiglu_fp8_fwd(const void* gate, const void* up, uint8
     return with_fp8(fp8_format, [&](auto f) {
       constexpr int FMT = decltype(f)::value;
       if (scale_mode == 0) return launch_swiglu_fp8_token<C, FMT>(gate, up, y_fp8, scale, rows, cols, st);
-      if (launch_swiglu_fp8_rows<C, FMT, true>(gate, up, y_fp8, nullptr, static_scale, rows, cols, st)) {
+      if (launch_swiglu_fp8_rows<C, FMT, true>(gate, up, y_fp8, scale, static_scale, rows, cols, st)) {
         return launch_status();
       }
       // Otherwise one flat stream over rows * cols elements.
@@ -448,7 +455,7 @@ extern "C" int32_t launch_swiglu_fp8_fwd(const void* gate, const void* up, uint8
             constexpr int kPer = kTabThreads * kTabUnroll;
             swiglu_fp8_static_flat<C, FMT, kTabThreads, kTabUnroll, true>
                 <<<flat_grid((nvec + kPer - 1) / kPer, 1, 1 << 20), kTabThreads, 0, st>>>(g4, u4, y_fp8,
-                                                                                          static_scale, nvec);
+                                                                                          static_scale, nvec, scale);
             tab = true;
           }
         }
@@ -456,13 +463,13 @@ extern "C" int32_t launch_swiglu_fp8_fwd(const void* gate, const void* up, uint8
           constexpr int UNROLL = 4;
           swiglu_fp8_static_flat<C, FMT, 256, UNROLL, false>
               <<<flat_grid((nvec + UNROLL - 1) / UNROLL, 256, 1 << 20), 256, 0, st>>>(g4, u4, y_fp8, static_scale,
-                                                                                      nvec);
+                                                                                      nvec, scale);
         }
         done = nvec * C::VEC;
       }
       if (done < n) {
         swiglu_fp8_static_scalar<C, FMT><<<flat_grid(n - done, 256, 4096), 256, 0, st>>>(gate, up, y_fp8, static_scale,
-                                                                                         done, n);
+                                                                                         done, n, scale);
       }
       return launch_status();
     });

@@ -54,8 +54,13 @@ def fp8_quant(
     x_fp8 = torch.empty((m, n), dtype=FP8_TORCH_DTYPES[fp8_format], device=device)
 
     if scale is not None:
-        native.fp8_quant_static_fwd(x, x_fp8, float(scale), fp8_format)
-        return x_fp8, torch.full((1,), float(scale), dtype=torch.float32, device=device)
+        # The kernel stores the scale into the returned [1] tensor (one launch);
+        # an empty x launches nothing, so its scale tensor is filled here.
+        scales = torch.empty(1, dtype=torch.float32, device=device)
+        native.fp8_quant_static_fwd(x, x_fp8, float(scale), fp8_format, scales)
+        if x.numel() == 0:
+            scales.fill_(float(scale))
+        return x_fp8, scales
 
     if granularity == "block":
         scales = torch.empty(

@@ -53,5 +53,10 @@ def rmsnorm_residual_fp8(
         scales = torch.empty(rows, dtype=torch.float32, device=x.device)
         native.rmsnorm_residual_fp8_fwd(x, residual, weight, y_fp8, scales, residual_out, eps, fp8_format, None)
         return y_fp8, scales.view(x.shape[:-1]), residual_out
-    native.rmsnorm_residual_fp8_fwd(x, residual, weight, y_fp8, None, residual_out, eps, fp8_format, float(scale))
-    return y_fp8, torch.full((1,), float(scale), dtype=torch.float32, device=x.device), residual_out
+    # The kernel stores the static scale into the returned [1] tensor (one
+    # launch); an empty x launches nothing, so its scale tensor is filled here.
+    scales = torch.empty(1, dtype=torch.float32, device=x.device)
+    native.rmsnorm_residual_fp8_fwd(x, residual, weight, y_fp8, scales, residual_out, eps, fp8_format, float(scale))
+    if x.numel() == 0:
+        scales.fill_(float(scale))
+    return y_fp8, scales, residual_out

@@ -38,5 +38,10 @@ def swiglu_fp8(
         scales = torch.empty(rows, dtype=torch.float32, device=gate.device)
         native.swiglu_fp8_fwd(gate, up, y_fp8, scales, fp8_format, None)
         return y_fp8, scales.view(gate.shape[:-1])
-    native.swiglu_fp8_fwd(gate, up, y_fp8, None, fp8_format, float(scale))
-    return y_fp8, torch.full((1,), float(scale), dtype=torch.float32, device=gate.device)
+    # The kernel stores the static scale into the returned [1] tensor (one
+    # launch); an empty gate launches nothing, so its scale tensor is filled here.
+    scales = torch.empty(1, dtype=torch.float32, device=gate.device)
+    native.swiglu_fp8_fwd(gate, up, y_fp8, scales, fp8_format, float(scale))
+    if gate.numel() == 0:
+        scales.fill_(float(scale))
+    return y_fp8, scales

@@ -112,13 +112,16 @@ int32_t launch_fp8_quant_token_fwd(const void* x, uint8_t* x_fp8, float* scale, 
 int32_t launch_fp8_quant_tensor_noalloc_fwd(const void* x, uint8_t* x_fp8, float* scale, int64_t m,
                                             int64_t n, int32_t dtype, int32_t fp8_format, void* stream);
 
-/* FP8 with a caller-given scale: x_fp8 = fp8(x / scale). */
-int32_t launch_fp8_quant_static_fwd(const void* x, uint8_t* x_fp8, float scale, int64_t m,
+/* FP8 with a caller-given scale: x_fp8 = fp8(x / scale). scale_out may be
+ * NULL; otherwise the launch also stores scale into scale_out[0] (the scale
+ * tensor a caller returns), so a static call is a single kernel. */
+int32_t launch_fp8_quant_static_fwd(const void* x, uint8_t* x_fp8, float scale, float* scale_out, int64_t m,
                                     int64_t n, int32_t dtype, int32_t fp8_format, void* stream);
 
 /* residual_out = x + residual, and the FP8 codes of y = rmsnorm(residual_out) * weight
  * (y rounded to dtype first; y itself is not written). scale_mode CCK_SCALE_TOKEN
- * writes scale[rows]; CCK_SCALE_STATIC uses static_scale. */
+ * writes scale[rows]; CCK_SCALE_STATIC uses static_scale and, when scale is not
+ * NULL, stores it into scale[0]. */
 int32_t launch_rmsnorm_residual_fp8_fwd(const void* x, const void* residual, const void* weight,
                                         uint8_t* y_fp8, float* scale, void* residual_out,
                                         int64_t rows, int64_t cols, float eps, float static_scale,

@@ -50,7 +50,7 @@ def test_empty_work_returns_success_without_device_calls():
     assert lib.launch_fp8_quant_block_fwd(None, None, None, 0, 16, 2, 3, None) == 0
     assert lib.launch_fp8_quant_tensor_fwd(None, None, None, None, 16, 0, 2, 3, None) == 0
     assert lib.launch_fp8_quant_token_fwd(None, None, None, 0, 16, 2, 3, None) == 0
-    assert lib.launch_fp8_quant_static_fwd(None, None, 0.05, 0, 16, 2, 3, None) == 0
+    assert lib.launch_fp8_quant_static_fwd(None, None, 0.05, None, 0, 16, 2, 3, None) == 0
     assert lib.launch_rmsnorm_residual_fp8_fwd(None, None, None, None, None, None, 0, 16, 1e-5, 0.0, 0, 2, 3, None) == 0
     assert lib.launch_swiglu_fp8_fwd(None, None, None, None, 0, 16, 0.0, 0, 2, 3, None) == 0
     assert lib.launch_token_gather_fwd(None, None, None, 0, 4096, 2, None) == 0
@@ -87,7 +87,7 @@ def test_unknown_tags_return_invalid_value_before_device_calls():
     assert lib.launch_fp8_quant_tensor_fwd(None, None, None, None, 4, 8, 2, 9, None) == 1
     assert lib.launch_fp8_quant_tensor_noalloc_fwd(None, None, None, 4, 8, 2, 9, None) == 1
     assert lib.launch_fp8_quant_tensor_noalloc_fwd(None, None, None, 1 << 40, 1 << 40, 2, 3, None) == 1  # m*n > int64
-    assert lib.launch_fp8_quant_static_fwd(None, None, 0.05, 4, 8, 2, 0, None) == 1
+    assert lib.launch_fp8_quant_static_fwd(None, None, 0.05, None, 4, 8, 2, 0, None) == 1
     assert lib.launch_rmsnorm_residual_fp8_fwd(None, None, None, None, None, None, 4, 8, 1e-5, 0.0, 2, 2, 3, None) == 1
     assert lib.launch_swiglu_fp8_fwd(None, None, None, None, 4, 8, 0.0, 7, 2, 3, None) == 1
     assert lib.cck_fp8_cvt_selftest(0, 16, 1, None, None) == 1
