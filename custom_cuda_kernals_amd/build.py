@@ -113,10 +113,20 @@ def native_compile_args(sanitize: bool = False) -> list[str]:
     return args
 
 
-def build_native() -> Path:
+def sanitize_requested() -> bool:
+    """CCK_SANITIZE=1 builds the binding with AddressSanitizer and
+    UndefinedBehaviorSanitizer. Python is not instrumented, so a process that
+    imports such a build must preload the runtimes: LD_PRELOAD="$(gcc
+    -print-file-name=libasan.so) $(gcc -print-file-name=libstdc++.so.6)" and
+    ASAN_OPTIONS=detect_leaks=0 (libstdc++ after libasan, so that the
+    sanitizer finds the real exception-throwing routine)."""
+    return os.environ.get("CCK_SANITIZE", "") == "1"
+
+
+def build_native(sanitize: bool | None = None) -> Path:
     out = native_ext_path()
     tmp = out.with_suffix(".tmp")
-    _run([*native_compile_args(), "-o", str(tmp)])
+    _run([*native_compile_args(sanitize_requested() if sanitize is None else sanitize), "-o", str(tmp)])
     os.replace(tmp, out)
     return out
 

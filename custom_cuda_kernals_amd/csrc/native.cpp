@@ -25,6 +25,7 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include <atomic>
 #include <cstdint>
 #include <optional>
 #include <sstream>
@@ -206,10 +207,17 @@ void check_dtype_matches(const char* name, const View& v, const View& expected, 
   }
 }
 
+// The stream handed to the most recent launcher (test hook: tells a test
+// which stream a call launched on, whether or not the runtime let that
+// stream overlap others).
+std::atomic<uintptr_t> last_launch_stream{0};
+
 // torch.cuda.current_stream(device_index).cuda_stream: the current HIP
 // stream of that device in c10's registry.
 void* current_stream(int64_t device_index) {
-  return c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device_index)).stream();
+  void* st = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device_index)).stream();
+  last_launch_stream.store(reinterpret_cast<uintptr_t>(st), std::memory_order_relaxed);
+  return st;
 }
 
 void check_launch(const char* launcher, int32_t err) {
@@ -675,6 +683,8 @@ PYBIND11_MODULE(_native, m) {
         py::arg("unpermute_index"), py::arg("num_experts"));
   m.def("moe_router_fwd", &moe_router_fwd, py::arg("logits"), py::arg("topk_weights"), py::arg("topk_indices"),
         py::arg("renormalize"));
+  m.def("_last_launch_stream", [] { return last_launch_stream.load(std::memory_order_relaxed); },
+        "Test hook: the hipStream_t (as an int) the most recent call launched on.");
   m.def("swiglu_fp8_fwd", &swiglu_fp8_fwd, py::arg("gate"), py::arg("up"), py::arg("y_fp8"), py::arg("scale"),
         py::arg("fp8_format"), py::arg("static_scale") = py::none());
 }

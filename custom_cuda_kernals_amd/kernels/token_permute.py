@@ -3,9 +3,10 @@
 ``token_gather`` and ``token_combine`` keep the reference signatures
 (custom_cuda/kernels/token_permute.py:19-44). ``compute_permutation`` is the
 index bookkeeping the reference keeps beside them
-(baselines/token_permute.py:55-70): one stable argsort of the expert
-assignments, computed with torch on the device; the kernels here do the
-bandwidth-bound row movement.
+(baselines/token_permute.py:55-70): a stable sort of the expert
+assignments. Given ``num_experts`` it runs the HIP counting-sort kernel
+(moe_permutation, one launch, three from 65536 entries); without it, the
+reference's torch ops (a stable argsort and its inverse) on the device.
 
 Additions: ``token_gather`` also moves FP8 rows (1-byte codes), and an
 index outside the source rows yields a zero row (gather) or drops its term

@@ -32,13 +32,66 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
 
 
-def test_reference_launchers_are_declared_with_reference_arity():
+# The reference's launchers, parameter by parameter, transcribed from its
+# headers with its CUDA types mapped to this ABI's: cudaStream_t -> void*
+# (the stream is an opaque pointer), cudaError_t (the return) -> int32_t.
+REFERENCE_LAUNCHERS = {
+    # csrc/includes/rmsnorm_residual.h:17-27
+    "launch_rmsnorm_residual_fwd": ["const void*", "const void*", "const void*", "void*", "void*", "int64_t",
+                                    "int64_t", "float", "int32_t", "void*"],
+    # csrc/includes/swiglu.h:16-22
+    "launch_swiglu_fwd": ["const void*", "const void*", "void*", "int64_t", "int32_t", "void*"],
+    # csrc/includes/rope.h:23-36
+    "launch_rope_fwd": ["const void*", "const void*", "const void*", "const void*", "void*", "void*", "int64_t",
+                        "int64_t", "int64_t", "int64_t", "int64_t", "int32_t", "void*"],
+    # csrc/includes/fp8_quant.h:41-49
+    "launch_fp8_quant_block_fwd": ["const void*", "uint8_t*", "float*", "int64_t", "int64_t", "int32_t", "int32_t",
+                                   "void*"],
+    # csrc/includes/fp8_quant.h:51-60
+    "launch_fp8_quant_tensor_fwd": ["const void*", "uint8_t*", "float*", "int32_t*", "int64_t", "int64_t",
+                                    "int32_t", "int32_t", "void*"],
+    # csrc/includes/token_permute.h:17-24
+    "launch_token_gather_fwd": ["const void*", "const int64_t*", "void*", "int64_t", "int64_t", "int32_t",
+                                "void*"],
+    # csrc/includes/token_permute.h:32-41
+    "launch_token_combine_fwd": ["const void*", "const int64_t*", "const float*", "void*", "int64_t", "int64_t",
+                                 "int64_t", "int32_t", "void*"],
+    # csrc/includes/moe_router.h:20-29
+    "launch_moe_router_fwd": ["const void*", "float*", "int64_t*", "int64_t", "int64_t", "int64_t", "int32_t",
+                              "int32_t", "void*"],
+}
+
+
+def test_reference_launchers_are_declared_with_reference_types():
+    """Every reference launcher is declared in include/custom_kernels_amd.h
+    with the reference's parameter types in the reference's order (and an
+    int32_t return: the declaration parser only matches those)."""
     d = _cck.declared_functions()
-    assert len(d["launch_rmsnorm_residual_fwd"]) == 10
-    assert len(d["launch_swiglu_fwd"]) == 6
-    assert len(d["launch_rope_fwd"]) == 13
-    assert len(d["launch_fp8_quant_block_fwd"]) == 8
-    assert len(d["launch_fp8_quant_tensor_fwd"]) == 9
+    for name, params in REFERENCE_LAUNCHERS.items():
+        assert name in d, name
+        assert d[name] == params, f"{name}: header {d[name]} != reference {params}"
+
+
+def test_parameter_type_parser_sees_a_changed_type():
+    """The check above fails on a one-type change: the parser distinguishes
+    the types it compares (a planted change to a copy of the header)."""
+    import os
+    import tempfile
+
+    text = open(_cck.HEADER).read()
+    changed = text.replace("void* y, void* residual_out, int64_t rows, int64_t cols,",
+                           "void* y, void* residual_out, int64_t rows, int32_t cols,", 1)
+    assert changed != text
+    with tempfile.NamedTemporaryFile("w", suffix=".h", delete=False) as f:
+        f.write(changed)
+    try:
+        saved = _cck.HEADER
+        _cck.HEADER = f.name
+        d = _cck.declared_functions()
+    finally:
+        _cck.HEADER = saved
+        os.unlink(f.name)
+    assert d["launch_rmsnorm_residual_fwd"] != REFERENCE_LAUNCHERS["launch_rmsnorm_residual_fwd"]
 
 
 def test_empty_work_returns_success_without_device_calls():

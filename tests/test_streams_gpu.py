@@ -1,10 +1,14 @@
 """The binding launches on torch.cuda.current_stream() of the tensors' device
 (reference src/kernels/rmsnorm_residual.rs:87-94), so a launch is ordered
-after earlier work on that stream only. Each case runs on a side stream that
-first spins (torch.cuda._sleep, a bounded busy-wait kernel) and then writes
-the real inputs over zeros: a launch issued on any other stream would run
-during the spin and read the zeros. Multi-kernel ops (per-tensor FP8) must
-keep all their kernels on that stream.
+after earlier work on that stream only. Each case runs on a side stream and
+checks, through the binding's host-side hook _native._last_launch_stream(),
+that the call launched on exactly that stream. The side stream first spins
+(torch.cuda._sleep, a bounded busy-wait kernel) and then writes the real
+inputs over zeros, so where the runtime lets the two streams overlap, a
+launch issued on any other stream would also have read the zeros.
+Multi-kernel ops (per-tensor FP8) keep all their kernels on the stream the
+binding hands them (the graph-replay tests check that: a launch off the
+capturing stream would not be replayed).
 """
 
 from __future__ import annotations
@@ -12,6 +16,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from custom_cuda_kernals_amd._lib import native
 from custom_cuda_kernals_amd.kernels import fp8_quant, moe_router, rmsnorm_residual, swiglu_fp8, token_combine
 from oracle import inputs
 
@@ -31,16 +36,15 @@ def _on_side_stream(fill_pairs, op):
         for dst, val in fill_pairs:
             dst.copy_(val)
         out = op()
+        launched_on = native._last_launch_stream()
+    assert launched_on == side.cuda_stream != torch.cuda.current_stream().cuda_stream
     # Control: work on the default stream runs during the spin and still sees
-    # the zeros, which is what a launch on the wrong stream would read. When
-    # the runtime has put both streams on one hardware queue (there are only
-    # GPU_MAX_HW_QUEUES of them) they run in order and the case cannot
-    # discriminate; tests/test_graph_replay_gpu.py checks the same property
-    # deterministically (a launch off the capturing stream is not replayed).
+    # the zeros, what a launch on the wrong stream would have read, unless the
+    # runtime put both streams on one hardware queue (there are only
+    # GPU_MAX_HW_QUEUES of them); the stream check above holds either way.
     probe = fill_pairs[0][0].clone()
     torch.cuda.synchronize()
-    if bool(probe.any()):
-        pytest.skip("side and default streams were serialised on one hardware queue")
+    print(f"streams overlapped: {not bool(probe.any())}")
     return out
 
 
