@@ -1,18 +1,29 @@
 // SiLU for the SwiGLU kernels and their device self-test, for gfx950.
 //
 // silu(g) = g * sigmoid(g), sigmoid = 1 / (1 + exp(-g)), in fp32 as the eager
-// formula (baselines/swiglu.py:107-112). The op is close to VALU-bound, so
-// sigmoid is built for instruction count: exp(-g) = 2^th * (1 + c) with one
-// v_exp_f32, and 1/(1+e) = one v_rcp_f32 plus a Newton step. For bf16 inputs,
-// th = -g*HI is exact (8-bit g times a 16-bit HI), so only the tiny
-// c = -g*LO*ln2 is rounded; other input types split the product with an fma.
-// Gates outside the fast range (exp(-g) near overflow, sigmoid subnormal, the
-// first-order correction no longer within an ulp, inf / NaN) use the IEEE
-// expf / division path.
+// formula (baselines/swiglu.py:107-112).
+//
+// fp32 gates (no storage rounding after the SiLU to absorb differences)
+// follow torch-CPU's float32 sigmoid exactly, as its vectorised loop
+// computes it: 1 / (1 + exp(0 - g)) with SLEEF's single-precision expf of
+// 1.0-ulp accuracy (the published xexpf algorithm: Cody-Waite reduction by
+// ln 2 in two parts, a degree-5 polynomial by Horner's rule, all with fused
+// multiply-adds, scaled by 2^q in two halves), an add and an IEEE division.
+//
+// bf16 / fp16 gates are rounded to their storage type after the SiLU, so
+// there sigmoid is built for instruction count (the op is close to
+// VALU-bound): exp(-g) = 2^th * (1 + c) with one v_exp_f32, and 1/(1+e) = one
+// v_rcp_f32 plus a Newton step. For bf16 inputs, th = -g*HI is exact (8-bit g
+// times a 16-bit HI), so only the tiny c = -g*LO*ln2 is rounded; fp16 splits
+// the product with an fma. Gates outside the fast range (exp(-g) near
+// overflow, sigmoid subnormal, the first-order correction no longer within an
+// ulp, inf / NaN) use the IEEE expf / division path.
 //
 // Everything here is compiled with fp contraction off (the pragma below also
 // holds for the rest of every file that includes this header).
 #pragma once
+
+#include <type_traits>
 
 #include "cdna4.hpp"
 
@@ -65,6 +76,47 @@ __device__ inline float recip_refined(float d) {
 
 __device__ inline float silu_exact(float g) { return g * (1.0f / (1.0f + __builtin_expf(-g))); }
 
+// SLEEF's xexpf (u10), operation for operation: q = rint(d / ln 2) as the
+// rounded product with RN(1 / ln 2), d - q ln 2 with ln 2 split in two
+// (L2U exact in a float with 16 trailing zero bits, L2L the rest), the
+// polynomial, 1 + (s^2 p(s) + s), and the scaling by 2^(q >> 1) 2^(q - (q >> 1))
+// (two steps, so no intermediate overflows); 0 below -104, +inf above 100.
+struct SleefExpf {
+  static constexpr float kRLn2 = 1.442695040888963407359924681001892137426645954152985934135449406931f;
+  static constexpr float kL2U = 0.693145751953125f;
+  static constexpr float kL2L = 1.428606765330187045e-06f;
+  static constexpr float kC0 = 0.000198527617612853646278381f, kC1 = 0.00139304355252534151077271f,
+                         kC2 = 0.00833336077630519866943359f, kC3 = 0.0416664853692054748535156f,
+                         kC4 = 0.166666671633720397949219f, kC5 = 0.5f;
+  __device__ static float pow2i(int e) { return bits_f32((uint32_t)(e + 127) << 23); }
+  __device__ static float eval(float d) {
+    // |d / ln 2| <= 151 wherever the result is not replaced below; the clamp
+    // keeps the conversion to int defined elsewhere (NaN d still gives NaN s).
+    const int q = (int)__builtin_rintf(__builtin_fminf(__builtin_fmaxf(d * kRLn2, -200.0f), 200.0f));
+    const float qf = (float)q;
+    float s = __builtin_fmaf(qf, -kL2U, d);
+    s = __builtin_fmaf(qf, -kL2L, s);
+    float u = kC0;
+    u = __builtin_fmaf(u, s, kC1);
+    u = __builtin_fmaf(u, s, kC2);
+    u = __builtin_fmaf(u, s, kC3);
+    u = __builtin_fmaf(u, s, kC4);
+    u = __builtin_fmaf(u, s, kC5);
+    u = 1.0f + __builtin_fmaf(s * s, u, s);
+    const int h = q >> 1;
+    u = u * pow2i(h);
+    u = u * pow2i(q - h);
+    u = d < -104.0f ? 0.0f : u;
+    return 100.0f < d ? __builtin_inff() : u;
+  }
+};
+
+// g * sigmoid(g) with torch-CPU's float32 vectorised sigmoid.
+__device__ inline float silu_sleef(float g) { return g * (1.0f / (1.0f + SleefExpf::eval(0.0f - g))); }
+
+template <class C>
+constexpr bool kSleefSilu = std::is_same_v<C, CodecF32>;
+
 template <class C>
 __device__ inline float silu_fast(float g) {
   return g * recip_refined(1.0f + exp_neg_fast<C>(g));
@@ -75,7 +127,11 @@ __device__ inline float silu_fast(float g) {
 // the neighbouring elements are.
 template <class C>
 __device__ inline float silu_one(float g) {
-  return __builtin_fabsf(g) <= SiluConsts<C>::kFastAbs ? silu_fast<C>(g) : silu_exact(g);
+  if constexpr (kSleefSilu<C>) {
+    return silu_sleef(g);
+  } else {
+    return __builtin_fabsf(g) <= SiluConsts<C>::kFastAbs ? silu_fast<C>(g) : silu_exact(g);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -188,6 +244,11 @@ __device__ inline void silu_vec(const u32x4& gw, const float* tab, float (&a)[C:
     if (SiluTableBF16::lookup8(gw, tab, a)) return;
   }
   C::unpack(gw, a);
+  if constexpr (kSleefSilu<C>) {
+#pragma unroll
+    for (int i = 0; i < C::VEC; ++i) a[i] = silu_sleef(a[i]);
+    return;
+  }
   float mx = 0.0f;
 #pragma unroll
   for (int i = 0; i < C::VEC; i += 2) mx = absmax2(mx, a[i], a[i + 1]);

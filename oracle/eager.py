@@ -38,9 +38,37 @@ def rmsnorm_residual(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tens
     return normed.to(dt) * weight, residual_out        # normed rounded to dt, then * weight in dt
 
 
+def sigmoid_f32_vectorised(g32: torch.Tensor) -> torch.Tensor:
+    """torch.sigmoid of a float32 tensor as torch's vectorised loop evaluates
+    it, for every element (oracle/sigmoid.py): torch itself on one thread
+    over a body that is a whole number of double vectors (so no element falls
+    into the loop's scalar tail), the restated vector path for the rest.
+    Multi-threaded torch would evaluate up to 2W - 1 elements at the end of
+    each thread's chunk with libm's expf instead."""
+    from oracle import sigmoid as osig
+
+    flat = g32.reshape(-1).contiguous()
+    n = flat.numel()
+    body = n - n % 64
+    out = torch.empty_like(flat)
+    if body:
+        prev = torch.get_num_threads()
+        torch.set_num_threads(1)
+        try:
+            out[:body] = torch.sigmoid(flat[:body])
+        finally:
+            torch.set_num_threads(prev)
+    if body < n:
+        out[body:] = torch.from_numpy(osig.sigmoid_vector(flat[body:].numpy()))
+    return out.view(g32.shape)
+
+
 def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     g32 = gate.to(torch.float32)
-    act = g32 * torch.sigmoid(g32)
+    # fp32 keeps every bit of the sigmoid, so its evaluation path is pinned
+    # (sigmoid_f32_vectorised); the narrower types round it away.
+    sig = sigmoid_f32_vectorised(g32) if gate.dtype == torch.float32 else torch.sigmoid(g32)
+    act = g32 * sig
     return act.to(gate.dtype) * up
 
 

@@ -6,14 +6,9 @@ applied to its output as stored in its dtype).
 * RMSNorm+FP8, every dtype: codes and scales bit-exact against the composed
   eager oracle (the kernel's y equals the eager y bit for bit), and
   residual_out bit-exact;
-* SwiGLU+FP8, bf16 / fp16: codes and scales bit-exact against the composed
-  eager oracle;
-* SwiGLU+FP8, fp32: codes and scales bit-exact against the oracle's
-  quantisation of the library's own unfused SwiGLU output; every code that
-  differs from the composed eager oracle must sit where that output differs
-  from torch's (torch-CPU's fp32 sigmoid is not correctly rounded; the
-  output itself is held to 1e-5 relative in test_swiglu_gpu.py). Mismatch
-  counts are printed.
+* SwiGLU+FP8, every dtype: codes and scales bit-exact against the composed
+  eager oracle (fp32 with torch-CPU's vectorised float32 sigmoid,
+  oracle/sigmoid.py).
 Workloads: BASELINE configs 3v and 5 (per-token and static 0.05) at full size,
 plus small and ragged shapes in all dtypes / formats.
 """
@@ -66,22 +61,9 @@ def _check_swiglu(g, u, fmt, static):
     n_bad = int((qn != strict).sum())
     print(f"\nswiglu+fp8 {tuple(g.shape)} {g.dtype} {fmt} static={static}: "
           f"{n_bad} of {strict.size} codes differ from the composed eager oracle")
-    if g.dtype != torch.float32:
-        assert_codes_equal(q, strict.reshape(q.shape))
-        s_strict = _scales_ref(s_strict, static)
-        assert_f32_bits_equal(s, s_strict.reshape(s.shape) if static is None else s_strict)
-        return
-    y_k = swiglu(gd, ud)
-    codes, s_ref = _quant(y_k, fmt, static)
-    assert_codes_equal(q, codes.reshape(q.shape))
-    assert_f32_bits_equal(s, s_ref.reshape(s.shape) if static is None else s_ref)
-    y_diff = ~bits_equal(y_k, y_ref).reshape(strict.shape)
-    code_diff = qn != strict
-    if static is None:
-        # a row whose scale moved can change any code of the row
-        row_moved = ~bits_equal(s.cpu(), torch.from_numpy(s_strict)).reshape(-1)
-        code_diff[row_moved.reshape(-1)] = False
-    assert not (code_diff & ~y_diff).any(), "a code differs where the fp32 SwiGLU output equals torch's"
+    assert_codes_equal(q, strict.reshape(q.shape))
+    s_strict = _scales_ref(s_strict, static)
+    assert_f32_bits_equal(s, s_strict.reshape(s.shape) if static is None else s_strict)
 
 
 @pytest.mark.parametrize("static", [None, 0.05])
