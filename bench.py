@@ -200,6 +200,18 @@ def _ops(torch, native):
     ops.append(Op("fp8_quant_tensor_noalloc", "fp8_tensor_noalloc_bf16_2048x4096", m1 * n1 * 3 + 4, mk1g,
                   tensor_noalloc, m1 * n1 * 3, [m1, n1]))
 
+    # One dynamic scale through the reference ABI at [8192, 4096] bf16 (not a
+    # BASELINE config): the input the one-pass form holds at its register
+    # capacity (16 vectors per thread over 256 workgroups on MI355X).
+    m1t, n1t = 8192, 4096
+
+    def mk1t():
+        return dict(x=rn(m1t, n1t), q=torch.empty(m1t, n1t, dtype=f8, device=dev), st=torch.empty(1, device=dev),
+                    amax=torch.zeros(1, dtype=torch.int32, device=dev))
+
+    ops.append(Op("fp8_quant_tensor_8192x4096", "fp8_tensor_bf16_8192x4096", m1t * n1t * 3 + 8, mk1t, tensor_fp8,
+                  m1t * n1t * 3, [m1t, n1t]))
+
     # Static scale 0.05 on its own (config 5's static mode fuses it into the producers).
     m1s, n1s = 16384, 4096
 
