@@ -507,6 +507,22 @@ def _cpu_time(fn, sets, budget_s: float):
     return times[len(times) // 2] * 1e-9, len(times)
 
 
+def _host_cpu(load_before: float) -> dict:
+    """The host the CPU baseline ran on: its CPU model, torch's vector
+    capability and the 1-minute load average before the timing (other
+    tenants of the host slow the baseline down)."""
+    import torch
+
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), model)
+    except OSError:
+        pass
+    return {"cpu": model, "capability": torch.backends.cpu.get_cpu_capability(),
+            "loadavg_1m_before": round(load_before, 2), "loadavg_1m_after": round(os.getloadavg()[0], 2)}
+
+
 def _cpu_baseline(budget_s: float):
     """The CPU oracle (torch-CPU / numpy restatements of the reference's eager
     baselines) timed on this host's cores, each op on a bounded row sample of
@@ -521,6 +537,7 @@ def _cpu_baseline(budget_s: float):
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     bf16 = torch.bfloat16
+    load_before = os.getloadavg()[0]
 
     def rot_sets(make, set_bytes, total=256 << 20, cap=64):
         return [make(i) for i in range(max(2, min(cap, total // set_bytes)))]
@@ -571,6 +588,7 @@ def _cpu_baseline(budget_s: float):
 
     head = per_op["rmsnorm_residual"]
     return {"value": head["TB_per_s"], "unit": "TB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "host": _host_cpu(load_before),
             "sample": f"oracle eager rmsnorm_residual on bf16 [{rows},{cols}] rows of the config-2 workload, "
                       f"rotating over 1 GiB of distinct inputs, median of {head['runs']} runs, "
                       f"{head['ms_per_run']:.3f} ms/run; per_op: every config op's oracle on a row sample",

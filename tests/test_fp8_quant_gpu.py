@@ -164,6 +164,31 @@ def test_tensor_amax_found_anywhere(shape, where):
     _check(x, "e4m3", "tensor")
 
 
+@pytest.mark.parametrize("via", ["api", "abi"])
+@pytest.mark.parametrize("where", ["workgroup0", "last"])
+@pytest.mark.parametrize("bits", [0x7F800001, 0xFF800001, 0x7FFFFFFF], ids=["snan1", "neg-snan1", "nan-max"])
+def test_tensor_one_pass_nan_patterns_of_the_exchange(bits, where, via):
+    """fp32 NaNs on the one-pass path ([2048, 4096]: 512 workgroups) whose
+    |x| bits equal the scale word's empty pattern (0x7f800001) or are the
+    largest NaN (0x7fffffff, next to the slots' empty pattern 0xffffffff), in
+    workgroup 0's share or the last workgroup's: the exchange ends, the scale
+    is NaN and every code equals the oracle's; through the reference ABI the
+    int32 ends up holding a NaN's bits."""
+    x = inputs.randn((2048, 4096), torch.float32, seed=91)
+    idx = 5 if where == "workgroup0" else x.numel() - 5
+    x.view(-1).view(torch.int32)[idx] = int(np.array([bits], dtype=np.uint32).view(np.int32)[0])
+    if via == "api":
+        _check(x, "e4m3", "tensor")
+        return
+    q = torch.empty(x.shape, dtype=torch.uint8, device="cuda")
+    word = torch.zeros(1, dtype=torch.int32, device="cuda")
+    scale = _tensor_abi(x.cuda(), q, word)
+    codes, s_ref = ofp8.quant_tensor(x.numpy(), "e4m3")
+    assert_codes_equal(q, codes)
+    assert_f32_bits_equal(scale, s_ref)
+    assert np.isnan(s_ref).all() and (int(word.item()) & 0x7FFFFFFF) > 0x7F800000
+
+
 def _tensor_abi(x_dev: torch.Tensor, q: torch.Tensor, scratch: torch.Tensor | None, fmt_tag: int = 3):
     from tests import _cck
 
