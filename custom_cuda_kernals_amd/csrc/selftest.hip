@@ -13,6 +13,11 @@
 //                           arithmetic SiLU entry by entry, and the table
 //                           lookup against the arithmetic path for all 2^16
 //                           bf16 gates.
+//   cck_sigmoid_selftest  - the fp32 SwiGLU's sigmoid (SLEEF's expf with
+//                           its scaling as one ldexp, and a reciprocal in
+//                           place of the division) against the
+//                           operation-for-operation form, for every fp32
+//                           bit pattern in [start, start + count).
 #include "launch.hpp"
 #include "silu.hpp"
 
@@ -175,6 +180,42 @@ __global__ __launch_bounds__(1024) void silu_table_selftest(unsigned long long* 
   if (checked) atomicAdd(&counters[5], checked);
 }
 
+// counters (unsigned long long[7]), g = every fp32 pattern in [start, start + count):
+//   [0] SleefExpf::eval_ldexp(g) != SleefExpf::eval(g)       (bitwise, NaN == NaN)
+//   [1] sigmoid_sleef(g) != sigmoid_sleef_ref(g)             (bitwise, NaN == NaN)
+//   [2] recip_refined(g) != 1 / g, for g in [1, kRecipRnLimit)
+//   [3] patterns checked in [2]
+//   [4..6] lowest mismatching pattern of [0..2] (init to ~0)
+__global__ __launch_bounds__(256) void sigmoid_selftest(uint64_t start, uint64_t count,
+                                                        unsigned long long* counters) {
+  unsigned long long n[3] = {0, 0, 0}, lo[3] = {~0ull, ~0ull, ~0ull}, checked = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * 256;
+  auto differ = [](float a, float b) {
+    return f32_bits(a) != f32_bits(b) && !(__builtin_isnan(a) && __builtin_isnan(b));
+  };
+  for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += stride) {
+    const uint64_t bits = start + i;
+    const float g = bits_f32((uint32_t)bits);
+    const bool bad[3] = {differ(SleefExpf::eval_ldexp(g), SleefExpf::eval(g)),
+                         differ(sigmoid_sleef(g), sigmoid_sleef_ref(g)),
+                         g >= 1.0f && g < kRecipRnLimit && differ(recip_refined(g), 1.0f / g)};
+    checked += g >= 1.0f && g < kRecipRnLimit;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      if (bad[c]) {
+        n[c] += 1;
+        lo[c] = lo[c] < bits ? lo[c] : bits;
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    if (n[c]) atomicAdd(&counters[c], n[c]);
+    if (lo[c] != ~0ull) atomicMin(&counters[4 + c], lo[c]);
+  }
+  if (checked) atomicAdd(&counters[3], checked);
+}
+
 }  // namespace
 }  // namespace cck
 
@@ -213,5 +254,14 @@ extern "C" int32_t cck_div_selftest(const float* xs, int64_t nx, const float* ss
 extern "C" int32_t cck_silu_table_selftest(unsigned long long* counters, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   silu_table_selftest<<<1, 1024, 0, st>>>(counters);
+  return launch_status();
+}
+
+extern "C" int32_t cck_sigmoid_selftest(uint64_t start, uint64_t count, unsigned long long* counters,
+                                        void* stream) {
+  if (count == 0) return (int32_t)hipSuccess;
+  if (start > 0xffffffffull || count > (1ull << 32) - start) return (int32_t)hipErrorInvalidValue;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  sigmoid_selftest<<<flat_grid((int64_t)(count / 64), 256, 8192), 256, 0, st>>>(start, count, counters);
   return launch_status();
 }

@@ -9,6 +9,10 @@
 // 1.0-ulp accuracy (the published xexpf algorithm: Cody-Waite reduction by
 // ln 2 in two parts, a degree-5 polynomial by Horner's rule, all with fused
 // multiply-adds, scaled by 2^q in two halves), an add and an IEEE division.
+// The kernels evaluate the same bits with fewer operations: the scaling as
+// one ldexp and the division as a Newton-refined reciprocal where that is
+// correctly rounded (both checked for every fp32 gate by
+// cck_sigmoid_selftest).
 //
 // bf16 / fp16 gates are rounded to their storage type after the SiLU, so
 // there sigmoid is built for instruction count (the op is close to
@@ -109,10 +113,48 @@ struct SleefExpf {
     u = d < -104.0f ? 0.0f : u;
     return 100.0f < d ? __builtin_inff() : u;
   }
+  // The same result with the scaling as one v_ldexp_f32. u * 2^(q >> 1) is
+  // exact (u is in [0.7, 1.5] and |q| <= 200), so eval rounds u * 2^q once,
+  // as ldexp does; cck_sigmoid_selftest compares the two for every float d.
+  __device__ static float eval_ldexp(float d) {
+    const float qf = __builtin_rintf(__builtin_fminf(__builtin_fmaxf(d * kRLn2, -200.0f), 200.0f));
+    float s = __builtin_fmaf(qf, -kL2U, d);
+    s = __builtin_fmaf(qf, -kL2L, s);
+    float u = kC0;
+    u = __builtin_fmaf(u, s, kC1);
+    u = __builtin_fmaf(u, s, kC2);
+    u = __builtin_fmaf(u, s, kC3);
+    u = __builtin_fmaf(u, s, kC4);
+    u = __builtin_fmaf(u, s, kC5);
+    u = 1.0f + __builtin_fmaf(s * s, u, s);
+    u = __builtin_amdgcn_ldexpf(u, (int)qf);
+    u = d < -104.0f ? 0.0f : u;
+    return 100.0f < d ? __builtin_inff() : u;
+  }
 };
 
+// Below this, recip_refined(d) for d >= 1 is the correctly rounded 1 / d
+// (cck_sigmoid_selftest compares it with IEEE division for every float in
+// [1, 2^64)).
+constexpr float kRecipRnLimit = 18446744073709551616.0f;  // 2^64
+
+// torch-CPU's float32 vectorised sigmoid, 1 / (1 + xexpf(0 - g)), with the
+// division as a correctly rounded reciprocal where that is checked (g above
+// about -44.4) and IEEE division elsewhere; the lanes that need the division
+// take it in a branch that a wave skips when none does.
+__device__ inline float sigmoid_sleef(float g) {
+  const float d = 1.0f + SleefExpf::eval_ldexp(0.0f - g);
+  float r = recip_refined(d);
+  if (!(d < kRecipRnLimit)) r = 1.0f / d;
+  return r;
+}
+
+// The operation-for-operation form (two-step scaling, IEEE division), the
+// reference of cck_sigmoid_selftest.
+__device__ inline float sigmoid_sleef_ref(float g) { return 1.0f / (1.0f + SleefExpf::eval(0.0f - g)); }
+
 // g * sigmoid(g) with torch-CPU's float32 vectorised sigmoid.
-__device__ inline float silu_sleef(float g) { return g * (1.0f / (1.0f + SleefExpf::eval(0.0f - g))); }
+__device__ inline float silu_sleef(float g) { return g * sigmoid_sleef(g); }
 
 template <class C>
 constexpr bool kSleefSilu = std::is_same_v<C, CodecF32>;
@@ -245,8 +287,23 @@ __device__ inline void silu_vec(const u32x4& gw, const float* tab, float (&a)[C:
   }
   C::unpack(gw, a);
   if constexpr (kSleefSilu<C>) {
+    // sigmoid_sleef per element, with one branch for the vector: the lanes
+    // where any 1 + e is at or above the reciprocal's checked range redo
+    // the four divisions in IEEE form (the same results where both apply).
+    float d[C::VEC], r[C::VEC];
+    bool wide = false;
 #pragma unroll
-    for (int i = 0; i < C::VEC; ++i) a[i] = silu_sleef(a[i]);
+    for (int i = 0; i < C::VEC; ++i) {
+      d[i] = 1.0f + SleefExpf::eval_ldexp(0.0f - a[i]);
+      r[i] = recip_refined(d[i]);
+      wide |= !(d[i] < kRecipRnLimit);
+    }
+    if (wide) {
+#pragma unroll
+      for (int i = 0; i < C::VEC; ++i) r[i] = 1.0f / d[i];
+    }
+#pragma unroll
+    for (int i = 0; i < C::VEC; ++i) a[i] = a[i] * r[i];
     return;
   }
   float mx = 0.0f;

@@ -221,6 +221,15 @@ int32_t cck_scale_selftest(uint64_t start, uint64_t count, int32_t fp8_format,
  * layout. */
 int32_t cck_silu_table_selftest(unsigned long long* counters, void* stream);
 
+/* Checks the fp32 SwiGLU's sigmoid (torch-CPU's: SLEEF's expf, 1 + e, a
+ * division) as the kernels evaluate it against the operation-for-operation
+ * form, for every fp32 bit pattern g in [start, start + count) (at most
+ * 2^32 - start): counters, 7 x u64, zeroed, with [4..6] preset to
+ * UINT64_MAX: [0] expf mismatches, [1] sigmoid mismatches, [2] reciprocal
+ * mismatches against IEEE 1 / g on [1, 2^64), [3] patterns checked in [2],
+ * [4..6] the lowest mismatching pattern of [0..2]. */
+int32_t cck_sigmoid_selftest(uint64_t start, uint64_t count, unsigned long long* counters, void* stream);
+
 /* Test hook (no reference counterpart): sets the number of polls (about
  * 1 us each) a waiting workgroup of the one-pass per-tensor FP8 form
  * (launch_fp8_quant_tensor_fwd and launch_fp8_quant_tensor_noalloc_fwd) makes

@@ -129,6 +129,13 @@ def test_hbm_stream_rejects_bad_arguments_before_device_calls():
     assert lib.cck_hbm_stream(5, None, None, None, None, 1000, None) == 1
 
 
+def test_sigmoid_selftest_rejects_a_range_past_2_to_32_before_device_calls():
+    lib = _cck.load()
+    assert lib.cck_sigmoid_selftest(0, 0, None, None) == 0
+    assert lib.cck_sigmoid_selftest((1 << 32) - 4, 8, None, None) == 1
+    assert lib.cck_sigmoid_selftest(1 << 32, 1, None, None) == 1
+
+
 def test_unknown_tags_return_invalid_value_before_device_calls():
     lib = _cck.load()
     assert lib.launch_rmsnorm_residual_fwd(None, None, None, None, None, 4, 8, 1e-5, 9, None) == 1

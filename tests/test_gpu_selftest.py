@@ -13,7 +13,14 @@ run through the C ABI diagnostics (csrc/selftest.hip):
 * the bf16 SiLU table of the SwiGLU+FP8 kernels: both fills against the
   arithmetic SiLU entry by entry, and the table lookup against the arithmetic
   path for all 2^16 bf16 gates (the arithmetic path itself is checked against
-  the oracle for every bf16 gate in test_swiglu_gpu.py).
+  the oracle for every bf16 gate in test_swiglu_gpu.py);
+* the fp32 SwiGLU's sigmoid as the kernels evaluate it (SLEEF's expf with its
+  scaling as one ldexp, and a Newton-refined reciprocal in place of the IEEE
+  division below 2^64) against the operation-for-operation form, for all
+  2^32 fp32 gates, and the reciprocal against IEEE 1 / d for every float in
+  [1, 2^64) (the operation-for-operation form is pinned to torch by
+  test_oracle_sigmoid.py and checked on the device against the oracle in
+  test_swiglu_gpu.py).
 """
 
 from __future__ import annotations
@@ -124,3 +131,20 @@ def test_silu_table_equals_arithmetic_silu():
     assert 0 < c[4] < 2 * 65536 // 8
     assert c[0] == 0 and c[1] == 0, f"fill mismatches {c[0]}/{c[1]}, lowest index {int(c[2])}"
     assert c[3] == 0, f"{c[3]} lookups differ from the arithmetic SiLU"
+
+
+def test_fp32_sigmoid_forms_agree_for_every_gate():
+    lib = _cck.load()
+    counters = torch.zeros(7, dtype=torch.int64, device="cuda")
+    counters[4:] = -1
+    stream = torch.cuda.current_stream().cuda_stream
+    chunk = 1 << 28
+    for start in range(0, 1 << 32, chunk):
+        assert lib.cck_sigmoid_selftest(start, chunk, counters.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    c = counters.cpu().numpy().view(np.uint64)
+    assert c[3] == 64 << 23, c[3]  # every float in [1, 2^64)
+    assert c[0] == 0, f"{c[0]} expf mismatches, lowest pattern {hex(int(c[4]))}"
+    assert c[1] == 0, f"{c[1]} sigmoid mismatches, lowest pattern {hex(int(c[5]))}"
+    assert c[2] == 0, f"{c[2]} reciprocal mismatches, lowest pattern {hex(int(c[6]))}"
+
