@@ -12,7 +12,9 @@
 //     a non-zero launcher status raises RuntimeError
 //     (src/kernels/error.rs:9-36);
 //   * launches on torch.cuda.current_stream(device_index).cuda_stream
-//     (src/kernels/rmsnorm_residual.rs:87-94); no synchronisation.
+//     (src/kernels/rmsnorm_residual.rs:87-94); no synchronisation. The
+//     tensors' device is made current for the launch and restored after it
+//     (a device guard, as torch's own ops use).
 // A torch.Tensor is read through its at::Tensor (device, contiguity, dtype,
 // data pointer, shape: no Python calls, about 0.2 us per tensor against 0.8
 // through the attributes); any other object goes through the Python
@@ -21,6 +23,7 @@
 // stream registry, which torch.cuda.current_stream reads too. The kernels are
 // reached through the C ABI only.
 #include <torch/csrc/autograd/python_variable.h>
+#include <c10/hip/HIPGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
@@ -212,13 +215,21 @@ void check_dtype_matches(const char* name, const View& v, const View& expected, 
 // stream overlap others).
 std::atomic<uintptr_t> last_launch_stream{0};
 
-// torch.cuda.current_stream(device_index).cuda_stream: the current HIP
+// One launch's context: the tensors' device is the current HIP device until
+// the launcher returns (as in torch's own ops, so the launchers' per-device
+// state, such as the one-pass grid's occupancy and the no-allocation array,
+// is that device's; the caller's current device is restored afterwards), and
+// st is torch.cuda.current_stream(device_index).cuda_stream, the current HIP
 // stream of that device in c10's registry.
-void* current_stream(int64_t device_index) {
-  void* st = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device_index)).stream();
-  last_launch_stream.store(reinterpret_cast<uintptr_t>(st), std::memory_order_relaxed);
-  return st;
-}
+struct Launch {
+  c10::hip::HIPGuard guard;
+  void* st;
+  explicit Launch(int64_t device_index)
+      : guard(static_cast<c10::DeviceIndex>(device_index)),
+        st(c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device_index)).stream()) {
+    last_launch_stream.store(reinterpret_cast<uintptr_t>(st), std::memory_order_relaxed);
+  }
+};
 
 void check_launch(const char* launcher, int32_t err) {
   if (err != 0) {
@@ -278,7 +289,8 @@ void rmsnorm_residual_fwd(py::handle x, py::handle residual, py::handle weight, 
                    "] (x's last dimension)");
   }
   const int64_t rows = product(xv.shape, 0, xv.shape.size() - 1);
-  void* st = current_stream(xv.device_index);
+  const Launch launch(xv.device_index);
+  void* st = launch.st;
   check_launch("launch_rmsnorm_residual_fwd",
                launch_rmsnorm_residual_fwd((const void*)xv.ptr, (const void*)rv.ptr, (const void*)wv.ptr,
                                            (void*)yv.ptr, (void*)rov.ptr, rows, cols, (float)eps,
@@ -297,7 +309,8 @@ void swiglu_fwd(py::handle gate, py::handle up, py::handle y) {
                    ", up=" + shape_str(uv.shape) + ", y=" + shape_str(yv.shape));
   }
   const int64_t n = product(gv.shape, 0, gv.shape.size());
-  void* st = current_stream(gv.device_index);
+  const Launch launch(gv.device_index);
+  void* st = launch.st;
   check_launch("launch_swiglu_fwd", launch_swiglu_fwd((const void*)gv.ptr, (const void*)uv.ptr,
                                                       (void*)yv.ptr, n, gv.dtype, st));
 }
@@ -341,7 +354,8 @@ void rope_fwd(py::handle q, py::handle k, py::handle cos, py::handle sin, py::ha
     shape_mismatch("cos/sin must have shape [" + std::to_string(seq_len) + ", " + std::to_string(half) +
                    "]; got cos=" + shape_str(cv.shape) + ", sin=" + shape_str(sv.shape));
   }
-  void* st = current_stream(qv.device_index);
+  const Launch launch(qv.device_index);
+  void* st = launch.st;
   check_launch("launch_rope_fwd",
                launch_rope_fwd((const void*)qv.ptr, (const void*)kv.ptr, (const void*)cv.ptr,
                                (const void*)sv.ptr, (void*)qov.ptr, (void*)kov.ptr, batch, seq_len,
@@ -377,7 +391,8 @@ void fp8_quant_block_fwd(py::handle x, py::handle x_fp8, py::handle scale, const
     shape_mismatch("scale shape " + shape_str(sv.shape) + " must be [" + std::to_string(nrb) + ", " +
                    std::to_string(ncb) + "] (ceil(M/128), ceil(N/128))");
   }
-  void* st = current_stream(xv.device_index);
+  const Launch launch(xv.device_index);
+  void* st = launch.st;
   check_launch("launch_fp8_quant_block_fwd",
                launch_fp8_quant_block_fwd((const void*)xv.ptr, (uint8_t*)qv.ptr, (float*)sv.ptr, m, n,
                                           xv.dtype, fmt, st));
@@ -401,7 +416,8 @@ void fp8_quant_tensor_fwd(py::handle x, py::handle x_fp8, py::handle scale, py::
     shape_mismatch("amax_scratch must have exactly 1 element; got shape " + shape_str(av->shape));
   }
   const int64_t m = xv.shape[0], n = xv.shape[1];
-  void* st = current_stream(xv.device_index);
+  const Launch launch(xv.device_index);
+  void* st = launch.st;
   check_launch("launch_fp8_quant_tensor_fwd",
                launch_fp8_quant_tensor_fwd((const void*)xv.ptr, (uint8_t*)qv.ptr, (float*)sv.ptr,
                                            av ? (int32_t*)av->ptr : nullptr, m, n, xv.dtype, fmt, st));
@@ -421,7 +437,8 @@ void fp8_quant_token_fwd(py::handle x, py::handle x_fp8, py::handle scale, const
   if (sv.shape != std::vector<int64_t>{m}) {
     shape_mismatch("scale shape " + shape_str(sv.shape) + " must be [" + std::to_string(m) + "] (one per row)");
   }
-  void* st = current_stream(xv.device_index);
+  const Launch launch(xv.device_index);
+  void* st = launch.st;
   check_launch("launch_fp8_quant_token_fwd",
                launch_fp8_quant_token_fwd((const void*)xv.ptr, (uint8_t*)qv.ptr, (float*)sv.ptr, m, n,
                                           xv.dtype, fmt, st));
@@ -448,7 +465,8 @@ void fp8_quant_static_fwd(py::handle x, py::handle x_fp8, double scale, const st
   check_2d_and_codes(xv, qv);
   float* so = static_scale_out(scale_out);
   const int64_t m = xv.shape[0], n = xv.shape[1];
-  void* st = current_stream(xv.device_index);
+  const Launch launch(xv.device_index);
+  void* st = launch.st;
   check_launch("launch_fp8_quant_static_fwd",
                launch_fp8_quant_static_fwd((const void*)xv.ptr, (uint8_t*)qv.ptr, (float)scale, so, m, n,
                                            xv.dtype, fmt, st));
@@ -494,7 +512,8 @@ void rmsnorm_residual_fp8_fwd(py::handle x, py::handle residual, py::handle weig
   }
   const int64_t rows = product(xv.shape, 0, xv.shape.size() - 1);
   float* sp = fused_scale_arg(scale, static_scale, rows);
-  void* st = current_stream(xv.device_index);
+  const Launch launch(xv.device_index);
+  void* st = launch.st;
   check_launch("launch_rmsnorm_residual_fp8_fwd",
                launch_rmsnorm_residual_fp8_fwd(
                    (const void*)xv.ptr, (const void*)rv.ptr, (const void*)wv.ptr, (uint8_t*)qv.ptr, sp,
@@ -518,7 +537,8 @@ void swiglu_fp8_fwd(py::handle gate, py::handle up, py::handle y_fp8, py::handle
   const int64_t cols = gv.shape.back();
   const int64_t rows = product(gv.shape, 0, gv.shape.size() - 1);
   float* sp = fused_scale_arg(scale, static_scale, rows);
-  void* st = current_stream(gv.device_index);
+  const Launch launch(gv.device_index);
+  void* st = launch.st;
   check_launch("launch_swiglu_fp8_fwd",
                launch_swiglu_fp8_fwd((const void*)gv.ptr, (const void*)uv.ptr, (uint8_t*)qv.ptr, sp, rows,
                                      cols, static_scale ? (float)*static_scale : 0.0f,
@@ -555,7 +575,8 @@ void token_gather_fwd(py::handle src, py::handle indices, py::handle dst) {
     shape_mismatch("indices shape " + shape_str(iv.shape) + " must be [" + std::to_string(dv.shape[0]) +
                    "] (dst's row count)");
   }
-  void* st = current_stream(sv.device_index);
+  const Launch launch(sv.device_index);
+  void* st = launch.st;
   check_launch("launch_token_gather_fwd",
                launch_token_gather_checked_fwd((const void*)sv.ptr, (const int64_t*)iv.ptr, (void*)dv.ptr,
                                                sv.shape[0], dv.shape[0], hidden, sv.dtype, st));
@@ -592,7 +613,8 @@ void token_combine_fwd(py::handle expert_output, py::handle unpermute_index, py:
     shape_mismatch("combined's row count (" + std::to_string(cv.shape[0]) + ") must match unpermute_index's [" +
                    std::to_string(n_tokens) + ", ...]");
   }
-  void* st = current_stream(ev.device_index);
+  const Launch launch(ev.device_index);
+  void* st = launch.st;
   check_launch("launch_token_combine_fwd",
                launch_token_combine_checked_fwd((const void*)ev.ptr, (const int64_t*)iv.ptr, (const float*)wv.ptr,
                                                 (void*)cv.ptr, ev.shape[0], n_tokens, k, hidden, ev.dtype, st));
@@ -619,7 +641,8 @@ void moe_permutation_fwd(py::handle topk_indices, py::handle permute_index, py::
   if (num_experts < 1 || num_experts > 256) {
     shape_mismatch("num_experts (" + std::to_string(num_experts) + ") must be in [1, 256]");
   }
-  void* st = current_stream(tv.device_index);
+  const Launch launch(tv.device_index);
+  void* st = launch.st;
   check_launch("launch_moe_permutation_fwd",
                launch_moe_permutation_fwd((const int64_t*)tv.ptr, (int64_t*)pv.ptr, (int64_t*)uv.ptr, n_tokens, k,
                                           num_experts, st));
@@ -650,7 +673,8 @@ void moe_router_fwd(py::handle logits, py::handle topk_weights, py::handle topk_
     shape_mismatch("num_experts (" + std::to_string(n_experts) +
                    ") exceeds this kernel's supported maximum of 256");
   }
-  void* st = current_stream(lv.device_index);
+  const Launch launch(lv.device_index);
+  void* st = launch.st;
   check_launch("launch_moe_router_fwd",
                launch_moe_router_fwd((const void*)lv.ptr, (float*)wv.ptr, (int64_t*)iv.ptr, n_tokens, n_experts, k,
                                      lv.dtype, renormalize ? 1 : 0, st));
