@@ -8,11 +8,30 @@ infrastructure only; the product never imports this module).
                              ((gathered.float() * w).sum(dim=1).to(dtype))
 * ``moe_router``          <- baselines/moe_router.py:117-128
                              (softmax in fp32, topk, optional renormalisation)
+* ``softmax_avx512``      torch-CPU's float32 softmax over the last dim as
+                          its AVX-512 kernel computes it (below)
+* ``moe_router_avx512``   ``moe_router`` with that softmax and the
+                          renormalising sum in ATen's row-sum order
+                          (oracle/rowsum.py): what torch computes on an
+                          AVX-512 host, whatever the test host is
 * ``*_fp64``              <- the fp64 ground truths (token_permute.py:229-232,
                              254-260; moe_router.py:140-148)
 * ``combine_sequential``  the combine with its sum written out: fp32
                           products added in j order onto +0.0, the order the
                           HIP kernel uses
+
+torch-CPU's float32 softmax (torch 2.10, ATen's vectorised last-dim kernel
+with 16-float AVX-512 vectors, the oracle's third-party dependency), per row
+of n values x:
+  m = max(x) (NaN-propagating);  e_i = xexpf(x_i - m), SLEEF's 1-ulp expf
+  (oracle/sigmoid.py);  the sum of e in 16 lane classes: for n >= 16 lane L
+  starts at e_L and adds e_{L+16}, e_{L+32}, ... in order over the whole
+  vectors, lanes L < n mod 16 then add the tail element 16 (n // 16) + L, and
+  the 16 lanes are combined as lane L + lane (L xor 8), then xor 4, 2, 1,
+  giving lane 0; for n < 16 the sum is e_0 + e_1 + ... in order;
+  p_i = e_i * RN(1 / sum).
+On an AVX2 host torch uses 8-float vectors (another order); the restatement
+fixes the AVX-512 one, which the GPU kernel follows.
 
 The torch ops are the reference oracle's own CPU kernels. Pinned by
 (tests/test_oracle_moe.py): golden vectors written from the reference's own
@@ -73,8 +92,60 @@ def moe_router(logits: torch.Tensor, k: int, renormalize: bool = True) -> tuple[
 
 
 def softmax_probs(logits: torch.Tensor) -> torch.Tensor:
-    """The router's fp32 probabilities (for tie / near-tie analysis in tests)."""
-    return F.softmax(logits.to(torch.float32), dim=-1)
+    """The router's fp32 probabilities as torch computes them on an AVX-512
+    host (for tie analysis in tests)."""
+    return torch.from_numpy(softmax_avx512(logits.to(torch.float32).numpy()))
+
+
+_LANES16 = 16
+
+
+def softmax_avx512(x: np.ndarray) -> np.ndarray:
+    """float32 [rows, n] -> float32 [rows, n]: torch-CPU's softmax over the
+    last dim with 16-float vectors (module docstring)."""
+    from oracle import sigmoid as osig
+
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, n = x.shape
+    if n == 0:
+        return x.copy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        m = np.max(x, axis=1)  # order-free; NaN-propagating like ATen's maximum
+        e = osig.sleef_expf((x - m[:, None]).astype(np.float32))
+        if n < _LANES16:
+            total = e[:, 0].copy()
+            for i in range(1, n):
+                total = (total + e[:, i]).astype(np.float32)
+        else:
+            full = n // _LANES16
+            acc = e[:, :_LANES16].copy()
+            for v in range(1, full):
+                acc = (acc + e[:, v * _LANES16:(v + 1) * _LANES16]).astype(np.float32)
+            r = n - full * _LANES16
+            if r:
+                acc[:, :r] = (acc[:, :r] + e[:, full * _LANES16:]).astype(np.float32)
+            lanes = np.arange(_LANES16)
+            for step in (8, 4, 2, 1):
+                acc = (acc + acc[:, lanes ^ step]).astype(np.float32)
+            total = acc[:, 0]
+        inv = (np.float32(1) / total).astype(np.float32)
+        return (e * inv[:, None]).astype(np.float32)
+
+
+def moe_router_avx512(logits: torch.Tensor, k: int, renormalize: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+    """baselines/moe_router.py:117-128 as torch computes it on an AVX-512
+    host: the restated softmax, torch's topk (its order among exactly equal
+    probabilities is its own), and the renormalising sum in ATen's row-sum
+    order followed by an IEEE division."""
+    from oracle import rowsum
+
+    probs = torch.from_numpy(softmax_avx512(logits.to(torch.float32).numpy()))
+    w, i = torch.topk(probs, k, dim=-1)
+    if renormalize and k > 0 and w.shape[0] > 0:
+        wn = w.numpy()
+        with np.errstate(invalid="ignore", divide="ignore"):
+            w = torch.from_numpy((wn / rowsum.row_sum(wn)[:, None]).astype(np.float32))
+    return w, i
 
 
 def token_gather_fp64(src: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:

@@ -11,7 +11,16 @@
   order onto +0.0 (the order the HIP kernel uses), bit for bit;
 * the router: probabilities sum to 1, weights descend, renormalised weights
   sum to 1, and a planted mistake (the softmax taken in the storage dtype)
-  is caught by the golden vectors.
+  is caught by the golden vectors;
+* the restated AVX-512 softmax and router (``softmax_avx512``,
+  ``moe_router_avx512``, the forms the HIP kernel follows) equal torch's own
+  bit for bit on an AVX-512 host: every row length from 1 to 300, values over
+  many scales, -inf / NaN entries, the router case table in three dtypes and
+  the golden vectors; planted mistakes (8-lane vectors, lanes combined in
+  order instead of the xor tree, a division by the sum instead of the
+  reciprocal's product, a correctly rounded exp instead of SLEEF's) disagree
+  with torch; and the serial form of ATen's row sum the kernel uses for the
+  renormalising sum (non-negative addends, n < 512) equals the stated order.
 """
 
 from __future__ import annotations
@@ -136,3 +145,145 @@ def test_router_invariants_and_fp64(renorm):
     w64, i64 = moe.moe_router_fp64(logits, 6, renorm)
     assert torch.equal(i, i64)
     torch.testing.assert_close(w.double(), w64, rtol=1e-5, atol=1e-7)
+
+
+@pytest.fixture(scope="module")
+def avx512():
+    if torch.backends.cpu.get_cpu_capability() != "AVX512":
+        pytest.skip("torch's softmax runs with 16-float vectors only on AVX-512 hosts")
+
+
+def _bits_equal(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    return (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))
+
+
+def test_softmax_avx512_equals_torch_for_every_length(avx512):
+    rng = np.random.default_rng(21)
+    for n in range(1, 301):
+        scale = [0.1, 1.0, 4.0, 30.0][n % 4]
+        x = (rng.standard_normal((8, n)) * scale).astype(np.float32)
+        got = moe.softmax_avx512(x)
+        ref = torch.softmax(torch.from_numpy(x), dim=-1).numpy()
+        assert _bits_equal(got, ref).all(), n
+
+
+def test_softmax_avx512_special_values(avx512):
+    rng = np.random.default_rng(22)
+    x = (rng.standard_normal((6, 160)) * 3).astype(np.float32)
+    x[0, 5] = -np.inf
+    x[1, :] = -np.inf          # all -inf: NaN row
+    x[2, 7] = np.nan
+    x[3, 100:] = -np.inf
+    x[4, 9] = 1e30             # one dominant logit
+    x[5, :] = 0.0              # all equal
+    got = moe.softmax_avx512(x)
+    ref = torch.softmax(torch.from_numpy(x), dim=-1).numpy()
+    assert _bits_equal(got, ref).all()
+
+
+ROUTER_CASES = [(2048, 8, 2, True), (2048, 160, 6, True), (1024, 32, 4, True), (257, 16, 2, True),
+                (64, 1, 1, True), (128, 256, 8, True), (256, 16, 2, False), (96, 256, 256, True),
+                (300, 100, 4, True), (50, 17, 3, True)]
+
+
+@pytest.mark.parametrize("dt", list(TAGS.values()), ids=list(TAGS))
+@pytest.mark.parametrize("case", ROUTER_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_router_avx512_equals_torch(avx512, case, dt):
+    t, e, k, renorm = case
+    logits = inputs.router_inputs(t, e, dt, seed=t + e + k)
+    w, i = moe.moe_router_avx512(logits, k, renorm)
+    w_ref, i_ref = moe.moe_router(logits, k, renorm)
+    assert torch.equal(w.view(torch.int32), w_ref.view(torch.int32))
+    assert torch.equal(i, i_ref)
+
+
+@pytest.mark.parametrize("tag", list(TAGS))
+@pytest.mark.parametrize("e,k,renorm", [(8, 2, True), (160, 6, True), (32, 4, False)])
+def test_router_avx512_golden(gold, tag, e, k, renorm):
+    key = f"router_{tag}_e{e}_k{k}_r{int(renorm)}"
+    w, i = moe.moe_router_avx512(_t(gold[f"{key}_logits"], TAGS[tag]), k, renorm)
+    assert np.array_equal(w.view(torch.int32).numpy(), gold[f"{key}_w"].view(np.int32))
+    assert np.array_equal(i.numpy(), gold[f"{key}_i"])
+
+
+def _softmax_variant(x, lanes=16, tree=True, divide=False, exact_exp=False):
+    from oracle import sigmoid as osig
+
+    x = x.astype(np.float32)
+    m = x.max(axis=1)
+    d = (x - m[:, None]).astype(np.float32)
+    e = np.exp(d.astype(np.float64)).astype(np.float32) if exact_exp else osig.sleef_expf(d)
+    n = x.shape[1]
+    full = n // lanes
+    acc = e[:, :lanes].copy()
+    for v in range(1, full):
+        acc = (acc + e[:, v * lanes:(v + 1) * lanes]).astype(np.float32)
+    r = n - full * lanes
+    if r:
+        acc[:, :r] = (acc[:, :r] + e[:, full * lanes:]).astype(np.float32)
+    if tree:
+        idx = np.arange(lanes)
+        step = lanes // 2
+        while step:
+            acc = (acc + acc[:, idx ^ step]).astype(np.float32)
+            step //= 2
+        total = acc[:, 0]
+    else:
+        total = acc[:, 0].copy()
+        for j in range(1, lanes):
+            total = (total + acc[:, j]).astype(np.float32)
+    if divide:
+        return (e / total[:, None]).astype(np.float32)
+    return (e * (np.float32(1) / total)[:, None]).astype(np.float32)
+
+
+@pytest.mark.parametrize("mistake", [dict(lanes=8), dict(tree=False), dict(divide=True), dict(exact_exp=True)],
+                         ids=["8-lane", "lanes-in-order", "divide", "exact-exp"])
+def test_softmax_planted_mistakes_disagree_with_torch(avx512, mistake):
+    x = (np.random.default_rng(23).standard_normal((2048, 160)) * 3).astype(np.float32)
+    ref = torch.softmax(torch.from_numpy(x), dim=-1).numpy()
+    assert _bits_equal(_softmax_variant(x), ref).all()  # the stated form itself
+    wrong = _softmax_variant(x, **mistake)
+    assert (~_bits_equal(wrong, ref)).sum() > 100
+
+
+def _small_row_sum_serial(v):
+    """The router kernel's serial form of ATen's row sum for n < 512
+    non-negative addends: 8-lane vectors in 4 slots, each slot one running
+    sum from zero (no 16-step block completes below 512), leftover vectors
+    into slot 0, then the trailing scalars and the 8 lanes; rows under 8 as
+    scalars in 4 slots."""
+    f = np.float32
+    n = len(v)
+    if n < 8:
+        s = n >> 2
+        p = [f(v[k]) if s else f(0) for k in range(4)]
+        for u in range(4 * s, n):
+            p[0] = f(p[0] + v[u])
+        return f(f(f(p[0] + p[1]) + p[2]) + p[3])
+    nv, total = n >> 3, f(0)
+    s = nv >> 2
+    for e in range(nv * 8, n):
+        total = f(total + v[e])
+    for lane in range(8):
+        p = [f(0)] * 4
+        for i in range(s):
+            for k in range(4):
+                p[k] = f(p[k] + v[(4 * i + k) * 8 + lane])
+        for vec in range(4 * s, nv):
+            p[0] = f(p[0] + v[vec * 8 + lane])
+        total = f(total + f(f(f(p[0] + p[1]) + p[2]) + p[3]))
+    return total
+
+
+def test_small_row_sum_serial_form_equals_the_stated_order():
+    from oracle import rowsum
+
+    rng = np.random.default_rng(24)
+    for n in list(range(1, 80)) + [100, 127, 128, 129, 255, 256, 257, 384, 511]:
+        v = (rng.random((4, n)) * np.exp2(rng.integers(-20, 20, (4, n)))).astype(np.float32)
+        want = rowsum.row_sum(v)
+        got = np.array([_small_row_sum_serial(row) for row in v], np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), n
