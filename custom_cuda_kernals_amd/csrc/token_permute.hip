@@ -3,9 +3,17 @@
 // Semantics (baselines/token_permute.py:215-217, 237-251):
 //   gather:   dst[i] = src[indices[i]]
 //   combine:  out[t] = T( sum_j  float(w[t,j]) * float(eo[unpermute_index[t,j]]) )
-// The combine rounds every product to fp32 and adds them in j order onto an
-// accumulator that starts at +0.0, which is the eager oracle's
-// (gathered.float() * w).sum(dim=1) on rows whose length is a multiple of 16.
+// The combine rounds every product to fp32 and sums them per output column
+// in the order torch-CPU's (gathered.float() * w).sum(dim=1) uses (ATen's
+// reduction of a contiguous [T, k, h] tensor over its middle dimension):
+//   * the leading columns it reduces as vector lanes (32-column chunks, the
+//     first 4 of rows of 4 to 7): one running sum over j = 0..k-1 from +0.0
+//     in ATen's block cascade (AtenCascade), which is plain j order for
+//     k <= 16;
+//   * the other columns: ATen's scalar form, four slots of every fourth j
+//     (aten_scalar_sum);
+//   * h == 1, where the reduced dimension is contiguous: ATen's row sum
+//     (aten_row_sum).
 //
 // Design: one workgroup per output row (64-512 threads, sized to the row).
 // The row's index (and weight) is workgroup-uniform and read once into SGPRs;
@@ -94,21 +102,129 @@ __global__ __launch_bounds__(256) void token_gather_elems(const E* __restrict__ 
   }
 }
 
+// ATen's block cascade of one float running sum (the fp32 sum kernel's
+// accumulation, also stated in oracle/rowsum.py): the steps fold into a0 in
+// blocks of 2^p; after each whole block a1 += a0 and a0 = 0, after every 2^p
+// blocks a2 += a1 and a1 = 0, after every 2^(2p) blocks a3 += a2 and a2 = 0;
+// the total is ((a0 + a1) + a2) + a3.
+struct AtenCascade {
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  // x is step number `step` (1-based) of the sum.
+  __device__ void add(float x, int64_t step, int p) {
+    a0 = a0 + x;
+    const int64_t m = (int64_t(1) << p) - 1;
+    if ((step & m) == 0) {
+      a1 = a1 + a0;
+      a0 = 0.0f;
+      if (((step >> p) & m) == 0) {
+        a2 = a2 + a1;
+        a1 = 0.0f;
+        if (((step >> (2 * p)) & m) == 0) {
+          a3 = a3 + a2;
+          a2 = 0.0f;
+        }
+      }
+    }
+  }
+  __device__ float total() const { return ((a0 + a1) + a2) + a3; }
+};
+
+// ATen's block size exponent for a sum of `steps` steps: max(4, ceil(log2
+// steps) / 4), with ceil(log2 m) taken as 1 for m <= 2.
+inline int aten_level_power(int64_t steps) {
+  int c = 1;
+  while (steps > 2 && (int64_t(1) << c) < steps) ++c;
+  return c / 4 > 4 ? c / 4 : 4;
+}
+
+// ATen's scalar form of a sum of n terms (term(j) gives term j): four slots
+// of every fourth term, each an AtenCascade with block exponent p, the n mod
+// 4 leftovers added to slot 0, then ((s0 + s1) + s2) + s3.
+template <class F>
+__device__ inline float aten_scalar_sum(int64_t n, int p, F&& term) {
+  AtenCascade sl[4];
+  const int64_t steps = n / 4;
+  for (int64_t i = 0; i < steps; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sl[q].add(term(4 * i + q), i + 1, p);
+  }
+  float s0 = sl[0].total();
+  for (int64_t j = 4 * steps; j < n; ++j) s0 = s0 + term(j);
+  return ((s0 + sl[1].total()) + sl[2].total()) + sl[3].total();
+}
+
+// ATen's row sum of n contiguous terms (oracle/rowsum.py): under 8 terms the
+// scalar form; otherwise 8-lane vectors in the scalar form's four slots per
+// lane (block exponent p8 for n / 32 steps), then 0 + the n mod 8 trailing
+// terms in order + the 8 lane totals in order. One thread, a pass per lane.
+template <class F>
+__device__ inline float aten_row_sum(int64_t n, int p4, int p8, F&& term) {
+  if (n < 8) return 0.0f + aten_scalar_sum(n, p4, term);
+  const int64_t nv = n / 8, steps = nv / 4;
+  float total = 0.0f;
+  for (int64_t e = nv * 8; e < n; ++e) total = total + term(e);
+  for (int l = 0; l < 8; ++l) {
+    AtenCascade sl[4];
+    for (int64_t i = 0; i < steps; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sl[q].add(term((4 * i + q) * 8 + l), i + 1, p8);
+    }
+    float s0 = sl[0].total();
+    for (int64_t v = 4 * steps; v < nv; ++v) s0 = s0 + term(v * 8 + l);
+    total = total + (((s0 + sl[1].total()) + sl[2].total()) + sl[3].total());
+  }
+  return total;
+}
+
+// The order parameters of one combine (host side).
+struct CombineOrder {
+  int64_t main_cols;  // leading columns summed as vector lanes
+  int p_main, p_slot, p_row;
+};
+
+inline CombineOrder combine_order(int64_t k, int64_t h) {
+  CombineOrder o;
+  o.main_cols = h >= 32 ? h - h % 32 : (h >= 4 && h < 8 ? 4 : 0);
+  o.p_main = aten_level_power(k);
+  o.p_slot = aten_level_power(k / 4);
+  o.p_row = aten_level_power(k / 32);
+  return o;
+}
+
+// One tail column of one token in ATen's scalar form (h == 1: the row sum).
+template <class C>
+__device__ inline float combine_scalar_column(const void* eo, const int64_t* it, const float* wt, int64_t k,
+                                              int64_t h, int64_t c, int64_t n_rows, const CombineOrder& o) {
+  auto term = [&](int64_t j) {
+    const int64_t r = it[j];
+    return r >= 0 && r < n_rows ? wt[j] * C::load1(eo, r * h + c) : 0.0f;
+  };
+  return h == 1 ? aten_row_sum(k, o.p_slot, o.p_row, term) : aten_scalar_sum(k, o.p_slot, term);
+}
+
 // Weighted combine on 16-byte vectors: one workgroup per token, VPL vectors
 // per thread per step; JU expert rows are loaded together before they are
-// accumulated in j order.
-template <class C, int THREADS, int VPL, int JU>
+// accumulated in j order (CASC: in ATen's block cascade, for k > 16). That is
+// torch's order for the main columns; the launcher then rewrites the other
+// (at most 31) columns with token_combine_elems on the same stream. Bounding
+// this kernel by the main columns instead measured 3 % slower at 4096 tokens
+// x hidden 7168 (76.0 against 73.5 us, k = 6) for the same instructions. A
+// dropped term (index outside the source rows) adds +0.0, which changes no
+// sum that starts at +0.0.
+template <class C, int THREADS, int VPL, int JU, bool CASC>
 __global__ __launch_bounds__(THREADS) void token_combine_vec(const u32x4* __restrict__ eo,
                                                              const int64_t* __restrict__ uidx,
                                                              const float* __restrict__ w,
                                                              u32x4* __restrict__ out, int64_t n_tokens,
-                                                             int64_t k, int64_t row_vecs, int64_t n_rows) {
+                                                             int64_t k, int64_t row_vecs, int64_t n_rows,
+                                                             int p_main) {
   constexpr int VEC = C::VEC;
   for (int64_t t = blockIdx.x; t < n_tokens; t += gridDim.x) {
     const int64_t* it = uidx + t * k;
     const float* wt = w + t * k;
     for (int64_t base = threadIdx.x; base < row_vecs; base += THREADS * VPL) {
       float acc[VPL][VEC];
+      AtenCascade cas[CASC ? VPL : 1][CASC ? VEC : 1];
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
 #pragma unroll
@@ -131,15 +247,29 @@ __global__ __launch_bounds__(THREADS) void token_combine_vec(const u32x4* __rest
         }
 #pragma unroll
         for (int u = 0; u < JU; ++u) {
-          if (!ok[u]) continue;
+          if constexpr (CASC) {
+            if (j0 + u >= k) continue;
 #pragma unroll
-          for (int v = 0; v < VPL; ++v) {
-            const int64_t c = base + THREADS * v;
-            if (c < row_vecs) {
-              float x[VEC];
-              C::unpack(raw[u][v], x);
+            for (int v = 0; v < VPL; ++v) {
+              const int64_t c = base + THREADS * v;
+              if (c < row_vecs) {
+                float x[VEC];
+                C::unpack(raw[u][v], x);
 #pragma unroll
-              for (int i = 0; i < VEC; ++i) acc[v][i] = acc[v][i] + wj[u] * x[i];
+                for (int i = 0; i < VEC; ++i) cas[v][i].add(ok[u] ? wj[u] * x[i] : 0.0f, j0 + u + 1, p_main);
+              }
+            }
+          } else {
+            if (!ok[u]) continue;
+#pragma unroll
+            for (int v = 0; v < VPL; ++v) {
+              const int64_t c = base + THREADS * v;
+              if (c < row_vecs) {
+                float x[VEC];
+                C::unpack(raw[u][v], x);
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) acc[v][i] = acc[v][i] + wj[u] * x[i];
+              }
             }
           }
         }
@@ -147,26 +277,42 @@ __global__ __launch_bounds__(THREADS) void token_combine_vec(const u32x4* __rest
 #pragma unroll
       for (int v = 0; v < VPL; ++v) {
         const int64_t c = base + THREADS * v;
+        if constexpr (CASC) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[v][i] = cas[v][i].total();
+        }
         if (c < row_vecs) st_stream(C::pack(acc[v]), out + t * row_vecs + c);
       }
     }
   }
 }
 
-template <class C>
-__global__ __launch_bounds__(256) void token_combine_elems(const void* __restrict__ eo,
-                                                           const int64_t* __restrict__ uidx,
-                                                           const float* __restrict__ w,
-                                                           void* __restrict__ out, int64_t n_tokens,
-                                                           int64_t k, int64_t h, int64_t n_rows) {
+// Columns c0..h-1 one per thread (any alignment): the main columns with
+// ATen's block cascade, the others in the scalar form (or h == 1: the row
+// sum).
+template <class C, int THREADS>
+__global__ __launch_bounds__(THREADS) void token_combine_elems(const void* __restrict__ eo,
+                                                               const int64_t* __restrict__ uidx,
+                                                               const float* __restrict__ w,
+                                                               void* __restrict__ out, int64_t n_tokens,
+                                                               int64_t k, int64_t h, int64_t c0, int64_t n_rows,
+                                                               CombineOrder o) {
   for (int64_t t = blockIdx.x; t < n_tokens; t += gridDim.x) {
-    for (int64_t c = threadIdx.x; c < h; c += 256) {
-      float acc = 0.0f;
-      for (int64_t j = 0; j < k; ++j) {
-        const int64_t r = uidx[t * k + j];
-        if (r >= 0 && r < n_rows) acc = acc + w[t * k + j] * C::load1(eo, r * h + c);
+    const int64_t* it = uidx + t * k;
+    const float* wt = w + t * k;
+    for (int64_t c = c0 + threadIdx.x; c < h; c += THREADS) {
+      float v;
+      if (c < o.main_cols) {
+        AtenCascade acc;
+        for (int64_t j = 0; j < k; ++j) {
+          const int64_t r = it[j];
+          acc.add(r >= 0 && r < n_rows ? wt[j] * C::load1(eo, r * h + c) : 0.0f, j + 1, o.p_main);
+        }
+        v = acc.total();
+      } else {
+        v = combine_scalar_column<C>(eo, it, wt, k, h, c, n_rows, o);
       }
-      C::store1(out, t * h + c, acc);
+      C::store1(out, t * h + c, v);
     }
   }
 }
@@ -239,6 +385,7 @@ constexpr int64_t kCombineWideTokens = 4096;
 int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, int64_t n_tokens,
                 int64_t k, int64_t h, int32_t dtype, int64_t n_rows, hipStream_t st) {
   if (n_tokens <= 0 || k <= 0 || h <= 0) return (int32_t)hipSuccess;
+  const CombineOrder order = combine_order(k, h);
   return with_codec(dtype, [&](auto codec) {
     using C = decltype(codec);
     const unsigned grid = row_grid(n_tokens);
@@ -247,12 +394,22 @@ int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, 
       // (9.4 us at T=2048, k=2, hidden 4096 bf16); deeper top-k: 2 per thread
       // (20.5 us at k=6); both measured on MI355X against 1-8 vectors and 1-8 rows.
       const int64_t rv = h / C::VEC;
+      const int64_t mv = order.main_cols / C::VEC;
       auto wide = [&](auto vpl) {
         constexpr int V = decltype(vpl)::value;
-        token_combine_vec<C, 512, V, 2><<<grid, 512, 0, st>>>(static_cast<const u32x4*>(eo), uidx, w,
-                                                            static_cast<u32x4*>(out), n_tokens, k, rv, n_rows);
+        token_combine_vec<C, 512, V, 2, false><<<grid, 512, 0, st>>>(
+            static_cast<const u32x4*>(eo), uidx, w, static_cast<u32x4*>(out), n_tokens, k, rv, n_rows, order.p_main);
       };
-      if (n_tokens >= kCombineWideTokens && (k <= 2 ? rv >= 512 : rv > 512) && rv <= 4 * 512) {
+      if (mv == 0) {
+        // Rows of 8 to 31 elements: scalar columns only.
+      } else if (k > 16) {
+        // Deeper sums take ATen's block cascade: one vector per thread.
+        with_row_threads<1, 512>(mv, [&](auto threads) {
+          constexpr int TH = decltype(threads)::value;
+          token_combine_vec<C, TH, 1, 2, true><<<grid, TH, 0, st>>>(
+              static_cast<const u32x4*>(eo), uidx, w, static_cast<u32x4*>(out), n_tokens, k, rv, n_rows, order.p_main);
+        });
+      } else if (n_tokens >= kCombineWideTokens && (k <= 2 ? mv >= 512 : mv > 512) && mv <= 4 * 512) {
         // Many tokens, rows of 512 to 2048 vectors (4096 to 16384 bf16):
         // 512-thread workgroups holding the row in one pass, measured on
         // MI355X (graph-replayed) against the shapes below: 35.0 vs 38.1 us at T=8192, k=2, hidden
@@ -260,28 +417,36 @@ int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, 
         // T=8192, k=8, hidden 7168; 412.7 vs 437.2 at hidden 16384 (but 10.4
         // vs 9.2 at T=2048, k=2, hidden 4096, 27.2 vs 26.3 at T=4096, k=8,
         // hidden 2048, and 159.5 vs 158.5 at T=16384, k=6, hidden 4096).
-        if (rv <= 512) {
+        if (mv <= 512) {
           wide(IntC<1>{});
-        } else if (rv <= 1024) {
+        } else if (mv <= 1024) {
           wide(IntC<2>{});
         } else {
           wide(IntC<4>{});
         }
       } else if (k <= 2) {
-        with_row_threads<4, 128>(rv, [&](auto threads) {
+        with_row_threads<4, 128>(mv, [&](auto threads) {
           constexpr int TH = decltype(threads)::value;
-          token_combine_vec<C, TH, 4, 2><<<grid, TH, 0, st>>>(static_cast<const u32x4*>(eo), uidx, w,
-                                                              static_cast<u32x4*>(out), n_tokens, k, rv, n_rows);
+          token_combine_vec<C, TH, 4, 2, false><<<grid, TH, 0, st>>>(
+              static_cast<const u32x4*>(eo), uidx, w, static_cast<u32x4*>(out), n_tokens, k, rv, n_rows, order.p_main);
         });
       } else {
-        with_row_threads<2, 256>(rv, [&](auto threads) {
+        with_row_threads<2, 256>(mv, [&](auto threads) {
           constexpr int TH = decltype(threads)::value;
-          token_combine_vec<C, TH, 2, 2><<<grid, TH, 0, st>>>(static_cast<const u32x4*>(eo), uidx, w,
-                                                              static_cast<u32x4*>(out), n_tokens, k, rv, n_rows);
+          token_combine_vec<C, TH, 2, 2, false><<<grid, TH, 0, st>>>(
+              static_cast<const u32x4*>(eo), uidx, w, static_cast<u32x4*>(out), n_tokens, k, rv, n_rows, order.p_main);
         });
       }
+      if (order.main_cols < h) {
+        // The h mod 32 scalar columns (at most 31) rewritten in a launch of
+        // their own, so the vector kernel keeps its registers (in the kernel,
+        // their code took 90 SGPRs instead of 64 and a second round of
+        // workgroups at 2048 tokens: 24.1 against 20.4 us, k = 6).
+        token_combine_elems<C, 64><<<grid, 64, 0, st>>>(eo, uidx, w, out, n_tokens, k, h, order.main_cols, n_rows,
+                                                        order);
+      }
     } else {
-      token_combine_elems<C><<<grid, 256, 0, st>>>(eo, uidx, w, out, n_tokens, k, h, n_rows);
+      token_combine_elems<C, 256><<<grid, 256, 0, st>>>(eo, uidx, w, out, n_tokens, k, h, 0, n_rows, order);
     }
     return launch_status();
   });

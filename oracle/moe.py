@@ -16,9 +16,8 @@ infrastructure only; the product never imports this module).
                           AVX-512 host, whatever the test host is
 * ``*_fp64``              <- the fp64 ground truths (token_permute.py:229-232,
                              254-260; moe_router.py:140-148)
-* ``combine_sequential``  the combine with its sum written out: fp32
-                          products added in j order onto +0.0, the order the
-                          HIP kernel uses
+* ``token_combine_aten``  the combine with torch-CPU's summation order
+                          written out (the order the HIP kernel follows)
 
 torch-CPU's float32 softmax (torch 2.10, ATen's vectorised last-dim kernel
 with 16-float AVX-512 vectors, the oracle's third-party dependency), per row
@@ -37,9 +36,8 @@ The torch ops are the reference oracle's own CPU kernels. Pinned by
 (tests/test_oracle_moe.py): golden vectors written from the reference's own
 baselines (tests/golden/reference_moe.npz), the permutation invariants
 (expert-sorted and stable, inverse of each other, round trip), the fp64
-closed forms within the reference's tolerances, and, for rows whose length is
-a multiple of 16, bit equality of ``token_combine`` and
-``combine_sequential``.
+closed forms within the reference's tolerances, and bit equality of
+``token_combine`` and ``token_combine_aten`` over row lengths and top-k.
 """
 
 from __future__ import annotations
@@ -65,22 +63,69 @@ def token_gather(src: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
 
 
 def token_combine(expert_output: torch.Tensor, unpermute_index: torch.Tensor, weights: torch.Tensor) -> torch.Tensor:
+    """The reference's formula on torch-CPU, evaluated on one thread: with
+    several threads torch may split a reduction of at least 32768 elements
+    over the hidden columns (in 32-column ranges, when the token count is
+    small), and a last range of 4 to 7 columns then sums its first 4 columns
+    in j order instead of the scalar form, so those bits depend on the host's
+    thread count. One thread gives the order every host shares."""
     if unpermute_index.numel() == 0:
         return torch.zeros(unpermute_index.shape[0], expert_output.shape[-1], dtype=expert_output.dtype)
-    gathered = expert_output[unpermute_index]
-    return (gathered.to(torch.float32) * weights.unsqueeze(-1)).sum(dim=1).to(expert_output.dtype)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        gathered = expert_output[unpermute_index]
+        return (gathered.to(torch.float32) * weights.unsqueeze(-1)).sum(dim=1).to(expert_output.dtype)
+    finally:
+        torch.set_num_threads(prev)
 
 
-def combine_sequential(expert_output: torch.Tensor, unpermute_index: torch.Tensor,
+def combine_main_columns(h: int) -> int:
+    """How many leading hidden columns torch-CPU's ``sum(dim=1)`` of a
+    contiguous [T, k, h] float32 tensor reduces as vector lanes (32-column
+    chunks; 4 columns for rows of 4 to 7); the rest take the scalar form."""
+    if h >= 32:
+        return h - h % 32
+    if 4 <= h < 8:
+        return 4
+    return 0
+
+
+def token_combine_aten(expert_output: torch.Tensor, unpermute_index: torch.Tensor,
                        weights: torch.Tensor) -> torch.Tensor:
-    """The same sum with an explicit order: acc = +0.0; acc += w_j * x_j for j = 0..k-1."""
-    eo = expert_output.to(torch.float32).numpy()
-    ui = unpermute_index.numpy()
-    w = weights.numpy().astype(np.float32)
-    acc = np.zeros((ui.shape[0], eo.shape[1]), dtype=np.float32)
-    for j in range(ui.shape[1]):
-        acc = (acc + (eo[ui[:, j]] * w[:, j:j + 1]).astype(np.float32)).astype(np.float32)
-    return torch.from_numpy(acc).to(expert_output.dtype)
+    """``(gathered.float() * w).sum(dim=1).to(dtype)`` in torch-CPU's own
+    order (torch 2.10 ATen, the oracle's third-party dependency): the products
+    rounded to float32, then per output column
+      * the leading ``combine_main_columns(h)`` columns: one running sum over
+        j = 0..k-1 in ATen's block cascade (blocks of 2^P steps, P = max(4,
+        ceil_log2(k) // 4), folded into a second, third and fourth
+        accumulator; oracle/rowsum.py), i.e. plain j order for k <= 16;
+      * the other columns: the scalar form, four slots of every fourth j
+        (each slot in the same cascade), the k mod 4 leftovers added to slot
+        0, then ((s0 + s1) + s2) + s3;
+      * h == 1 (the reduced dimension is contiguous): the row sum over k.
+    Pinned against torch by tests/test_oracle_moe.py."""
+    from oracle import rowsum
+
+    t, k = unpermute_index.shape
+    h = expert_output.shape[-1]
+    dt = expert_output.dtype
+    if t == 0 or k == 0:
+        return torch.zeros(t, h, dtype=dt)
+    prod = (expert_output.to(torch.float32)[unpermute_index] * weights.to(torch.float32).unsqueeze(-1)).numpy()
+    out = np.empty((t, h), np.float32)
+    if h == 1:
+        out[:, 0] = rowsum.row_sum(prod[:, :, 0])
+        return torch.from_numpy(out).to(dt)
+    cols = np.ascontiguousarray(prod.transpose(0, 2, 1))  # [t, h, k]
+    mc = combine_main_columns(h)
+    if mc:
+        u = cols[:, :mc].reshape(t * mc, k, 1, 1)
+        out[:, :mc] = rowsum._fold_slots(u)[:, 0, 0].reshape(t, mc)
+    if mc < h:
+        u = cols[:, mc:].reshape(t * (h - mc), k, 1)
+        out[:, mc:] = (np.float32(0) + rowsum._slot_sum(u)[:, 0]).reshape(t, h - mc)
+    return torch.from_numpy(out).to(dt)
 
 
 def moe_router(logits: torch.Tensor, k: int, renormalize: bool = True) -> tuple[torch.Tensor, torch.Tensor]:

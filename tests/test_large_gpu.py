@@ -192,6 +192,6 @@ def test_token_gather_and_combine_past_2g():
     spans = [slice(0, 48), slice(t // 2 - 24, t // 2 + 24), slice(t - 48, t)]
     assert all((u_cpu[sl] >= BIG // h).any() for sl in spans), "each span reads expert rows past element 2^31"
     for sl in spans:
-        # rows of 4096 elements (a multiple of 16): torch's CPU sum adds in j order, as the kernel does
+        # rows of 4096 elements, k = 2: torch's CPU sum adds in j order, as the kernel does
         ref = moe.token_combine(eo_cpu, u_cpu[sl], w_cpu[sl])
         assert bits_equal(out[sl].cpu(), ref).all(), f"combine tokens {sl}"

@@ -6,9 +6,11 @@
   combine round trip with unit weights is the identity
   (tests/test_token_permute.py:88-126 in the reference);
 * fp64 closed forms within the reference's tolerances (its TOLERANCES tables);
-* the combine's summation order: for rows whose length is a multiple of 16,
-  torch's (gathered.float() * w).sum(dim=1) equals fp32 products added in j
-  order onto +0.0 (the order the HIP kernel uses), bit for bit;
+* the combine's summation order (``token_combine_aten``, the order the HIP
+  kernel follows) equals torch's (gathered.float() * w).sum(dim=1) bit for
+  bit on the golden vectors and over row lengths 1-69 and 4096-4127 and top-k
+  1-600, and planted mistakes (j order on every column, the four-slot form on
+  every column, no block cascade) disagree with torch;
 * the router: probabilities sum to 1, weights descend, renormalised weights
   sum to 1, and a planted mistake (the softmax taken in the storage dtype)
   is caught by the golden vectors;
@@ -101,9 +103,8 @@ def test_combine_golden_and_order(gold, tag, k, h):
     eo, ui, w = _t(gold[f"{key}_eo"], dt), torch.from_numpy(gold[f"{key}_ui"]), _t(gold[f"{key}_w"], torch.float32)
     out = moe.token_combine(eo, ui, w)
     assert np.array_equal(_bits(out), gold[f"{key}_out"].view(_bits(out).dtype))
-    if h % 16 == 0:
-        assert torch.equal(moe.combine_sequential(eo, ui, w).view(torch.int16 if dt != torch.float32 else torch.int32),
-                           out.view(torch.int16 if dt != torch.float32 else torch.int32))
+    aten = moe.token_combine_aten(eo, ui, w)
+    assert np.array_equal(_bits(aten), gold[f"{key}_out"].view(_bits(out).dtype))
 
 
 @pytest.mark.parametrize("dt,rtol,atol", [(torch.float32, 1e-4, 1e-4), (torch.float16, 1e-2, 1e-2),
@@ -287,3 +288,53 @@ def test_small_row_sum_serial_form_equals_the_stated_order():
         want = rowsum.row_sum(v)
         got = np.array([_small_row_sum_serial(row) for row in v], np.float32)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), n
+
+
+def _combine_variant(eo, ui, w, mode):
+    """Planted mistakes of the combine order: "seq" (j order on every
+    column), "slot4" (the four-slot form on every column), "flat" (no block
+    cascade on the vector columns)."""
+    from oracle import rowsum
+
+    prod = (eo.float()[ui] * w.unsqueeze(-1)).numpy()
+    t, k, h = prod.shape
+    cols = np.ascontiguousarray(prod.transpose(0, 2, 1))
+    if mode == "seq" or mode == "flat":
+        acc = np.zeros((t, h), np.float32)
+        for j in range(k):
+            acc = (acc + cols[:, :, j]).astype(np.float32)
+        if mode == "flat":
+            mc = moe.combine_main_columns(h)
+            u = cols[:, mc:].reshape(t * (h - mc), k, 1)
+            acc[:, mc:] = (np.float32(0) + rowsum._slot_sum(u)[:, 0]).reshape(t, h - mc)
+        return acc
+    u = cols.reshape(t * h, k, 1)
+    return (np.float32(0) + rowsum._slot_sum(u)[:, 0]).reshape(t, h)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_combine_aten_order_equals_torch(dt):
+    rng = np.random.default_rng(31)
+    for h in list(range(1, 70)) + [96, 100, 4096, 4104, 4127]:
+        for k in (1, 2, 3, 4, 6, 8, 16, 17, 64, 65, 257, 600):
+            if h * k > 160000:
+                continue
+            t = 6
+            eo = torch.from_numpy((rng.standard_normal((t * k, h)) * np.exp2(rng.integers(-6, 6, (t * k, h))))
+                                  .astype(np.float32)).to(dt)
+            ui = torch.from_numpy(rng.permutation(t * k).reshape(t, k))
+            w = torch.from_numpy(rng.random((t, k)).astype(np.float32))
+            assert np.array_equal(_bits(moe.token_combine_aten(eo, ui, w)), _bits(moe.token_combine(eo, ui, w))), (h, k)
+
+
+@pytest.mark.parametrize("mode,h,k", [("seq", 100, 6), ("seq", 16, 8), ("slot4", 4096, 6), ("flat", 4096, 40)])
+def test_combine_planted_order_mistakes_disagree_with_torch(mode, h, k):
+    rng = np.random.default_rng(32)
+    t = 64
+    eo = torch.from_numpy((rng.standard_normal((t * k, h)) * np.exp2(rng.integers(-8, 8, (t * k, h))))
+                          .astype(np.float32))
+    ui = torch.from_numpy(rng.permutation(t * k).reshape(t, k))
+    w = torch.from_numpy(rng.random((t, k)).astype(np.float32))
+    ref = moe.token_combine(eo, ui, w).numpy()
+    wrong = _combine_variant(eo, ui, w, mode)
+    assert (wrong.view(np.uint32) != ref.view(np.uint32)).sum() > 20

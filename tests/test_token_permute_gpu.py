@@ -2,9 +2,10 @@
 restating baselines/token_permute.py:55-70, 215-217, 237-251).
 
 * gather is byte movement: bit-exact for every dtype (and FP8 rows);
-* combine: bit-exact where rows are a multiple of 16 elements (the oracle's
-  torch sum then adds in j order, as the kernel does); elsewhere within one
-  storage ulp (tests/_parity.py ULP_TOL); fp32 always within 1e-6 relative;
+* combine: bit-exact for every row length, top-k and dtype, against torch's
+  own sum and against its stated order (oracle/moe.py token_combine_aten: j
+  order with ATen's block cascade on the columns torch reduces as vector
+  lanes, its four-slot scalar form on the rest);
 * the reference's case tables (baselines/token_permute.py:128-167) in three
   dtypes, its vector-tail sweep (tests/test_token_permute_kernel.py:107-137),
   the permute -> unpermute round trip, and index hygiene (out-of-range
@@ -69,31 +70,17 @@ def test_gather_out_of_range_rows_are_zero():
 
 
 def _check_combine(eo, ui, w):
-    """Bit-exact against the kernel's defined order (fp32 products added in j
-    order onto +0.0, one rounding to the storage type) for every row length,
-    and against torch's sum, which takes the same order when the row length
-    is a multiple of 16. Otherwise torch's tail path adds in another order;
-    two fp32 orders of a k-term sum differ by at most a few fp32 ulps of
-    sum_j |w_j x_j|, so there the bound is one storage ulp of that magnitude
-    (not of the result, which cancellation can make arbitrarily small)."""
+    """Bit-exact against torch's (gathered.float() * w).sum(dim=1) and
+    against its stated order (oracle/moe.py token_combine_aten), one rounding
+    to the storage type."""
     out = token_combine(eo.cuda(), ui.cuda(), w.cuda()).cpu()
     ref = moe.token_combine(eo, ui, w)
     assert out.shape == ref.shape and out.dtype == eo.dtype
     if out.numel() == 0:
         return None
-    assert bits_equal(out, moe.combine_sequential(eo, ui, w)).all(), "kernel differs from the j-order sum"
-    if eo.shape[1] % 16 == 0:
-        assert bits_equal(out, ref).all()
-        return 1.0
-    # |sum_A - sum_B| <= 2 (k - 1) 2^-24 mag for two fp32 orders (k <= 8 here), plus
-    # at most one storage ulp of the result (|result| <= mag) when the two
-    # straddle a rounding boundary.
-    mag = (eo.float()[ui].abs() * w.abs().unsqueeze(-1)).sum(dim=1).double()
-    ulp = {torch.float32: 0.0, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[eo.dtype]
-    diff = (out.double() - ref.double()).abs()
-    bound = (ulp + 2.0 ** -19) * mag + 1e-30
-    assert bool((diff <= bound).all()), f"max diff / magnitude {float((diff / mag.clamp_min(1e-30)).max())}"
-    return float(bits_equal(out, ref).mean())
+    assert bits_equal(out, moe.token_combine_aten(eo, ui, w)).all(), "kernel differs from ATen's order"
+    assert bits_equal(out, ref).all(), "kernel differs from torch's sum"
+    return 1.0
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
@@ -104,11 +91,25 @@ def test_combine_matches_oracle(case, dtype):
     _check_combine(eo, ui, w)
 
 
+@pytest.mark.parametrize("k", [3, 6, 8])
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
-def test_combine_vector_tails(dtype):
-    for h in list(range(1, 20)) + [31, 32, 33, 127, 128, 129]:
-        eo, ui, w = inputs.combine_inputs(17, 3, h, dtype, seed=h)
+def test_combine_vector_tails(dtype, k):
+    """Row lengths around every vector and 32-column boundary: the scalar
+    four-slot columns (k >= 4 orders them differently from j order)."""
+    for h in list(range(1, 20)) + [24, 31, 32, 33, 40, 63, 64, 65, 127, 128, 129, 4104]:
+        eo, ui, w = inputs.combine_inputs(17, k, h, dtype, seed=h + k)
         _check_combine(eo, ui, w)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("t,k,h", [(64, 17, 4096), (32, 20, 4104), (32, 65, 512), (16, 256, 136), (8, 300, 40),
+                                   (16, 9, 1), (8, 40, 1), (4, 600, 1), (8, 1100, 64)])
+def test_combine_deep_topk_block_cascade(t, k, h, dtype):
+    """k > 16: ATen folds each running sum in 16-step blocks (the vector
+    columns) and each of the four slots in 16-step blocks (the scalar
+    columns); h == 1 sums each token's k terms as a contiguous row."""
+    eo, ui, w = inputs.combine_inputs(t, k, h, dtype, seed=t + k + h)
+    _check_combine(eo, ui, w)
 
 
 def test_combine_out_of_range_terms_are_dropped():
@@ -262,7 +263,7 @@ def test_fp8_dispatch_quantise_once_then_gather(t, k, e, h):
 def test_combine_many_tokens(k, h, dtype):
     """4100 tokens: the 512-thread one-pass shape for rows of 4096-16384
     elements (and the default shapes beside it), checked on token slices at
-    the start, the middle and the end against the explicit j-order sum."""
+    the start, the middle and the end against ATen's order."""
     t = 4100
     g = torch.Generator(device="cuda").manual_seed(k * h)
     eo = torch.randn(t * k, h, device="cuda", generator=g).to(dtype)
@@ -273,5 +274,5 @@ def test_combine_many_tokens(k, h, dtype):
     for sl in (slice(0, 24), slice(2000, 2024), slice(t - 24, t)):
         rows = ui[sl].reshape(-1)
         local = torch.arange(rows.numel()).view(-1, k)
-        ref = moe.combine_sequential(eo[rows].cpu(), local, w[sl].cpu())
+        ref = moe.token_combine_aten(eo[rows].cpu(), local, w[sl].cpu())
         assert bits_equal(out[sl].cpu(), ref).all(), sl

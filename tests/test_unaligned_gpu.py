@@ -115,7 +115,7 @@ def test_token_gather_combine_unaligned(dtype):
     eo, ui, w = inputs.combine_inputs(30, 3, 264, dtype, seed=10)
     out = _empty_off((30, 264), dtype)
     native.token_combine_fwd(_off(eo), ui.cuda(), w.cuda(), out)
-    assert bits_equal(out.cpu(), moe.combine_sequential(eo, ui, w)).all()
+    assert bits_equal(out.cpu(), moe.token_combine_aten(eo, ui, w)).all()
 
 
 @pytest.mark.parametrize("cols", [64, 1000, 2048, 4096, 11008])
