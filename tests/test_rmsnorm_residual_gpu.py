@@ -6,9 +6,9 @@ baselines/rmsnorm_residual.py:123-136).
   fp32 order (oracle/rowsum.py states it; tests/test_oracle_rowsum.py pins
   it against torch), so the variance, rsqrt and every rounding point match.
   The one-ulp bound (bf16 2^-7, fp16 2^-10, fp32 1e-5) is also checked.
-  Torch splits the sum of a single row of 32768 or more elements across
-  threads, so those rows are not used here (every case has 2+ rows or a
-  shorter row).
+  Torch may split the sum of a single row of 32768 or more elements across
+  threads, in an order that depends on the host's thread count; for those
+  rows the oracle runs on one thread, the serial order the kernel follows.
 Shapes: the reference's standard + edge cases (baselines/rmsnorm_residual.py:75-91),
 row lengths that reach every part of the summation order (8-lane vector
 tail, leftover vectors, trailing steps, acc2 / acc3 levels, the 32-step
@@ -108,6 +108,18 @@ def test_unaligned_and_long_rows(dtype):
 def test_every_row_shape_bucket(cols, dtype):
     x, r, w = inputs.rmsnorm_inputs(5, cols, dtype, seed=cols)
     _run(x, r, w, 1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("cols", [32768, 65536, (1 << 20) + 13])
+def test_single_long_row_against_one_thread_torch(cols, dtype):
+    x, r, w = inputs.rmsnorm_inputs(1, cols, dtype, seed=cols + 3)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        _run(x, r, w, 1e-5)
+    finally:
+        torch.set_num_threads(prev)
 
 
 def test_rejections():
