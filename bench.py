@@ -519,7 +519,19 @@ def _host_cpu(load_before: float) -> dict:
             model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), model)
     except OSError:
         pass
-    return {"cpu": model, "capability": torch.backends.cpu.get_cpu_capability(),
+    quota = None  # CPUs the cgroup may use (cgroup v2 cpu.max, else v1 cfs quota / period)
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()
+        quota = None if q == "max" else round(int(q) / int(period), 2)
+    except (OSError, ValueError):
+        try:
+            with open("/sys/fs/cgroup/cpu/cpu.cfs_quota_us") as f, open("/sys/fs/cgroup/cpu/cpu.cfs_period_us") as g:
+                q, period = int(f.read()), int(g.read())
+            quota = None if q < 0 else round(q / period, 2)
+        except (OSError, ValueError):
+            pass
+    return {"cpu": model, "capability": torch.backends.cpu.get_cpu_capability(), "cgroup_cpu_quota": quota,
             "loadavg_1m_before": round(load_before, 2), "loadavg_1m_after": round(os.getloadavg()[0], 2)}
 
 
