@@ -158,7 +158,12 @@ def test_moe_ops_graph():
     eo, ui, w = [t.cuda() for t in sets_c[0]]
     out = torch.empty(256, 4096, dtype=BF16, device="cuda")
     _replay_matches_eager([eo, ui, w], [out], lambda: native.token_combine_fwd(eo, ui, w, out), sets_c)
-    sets_r = [[inputs.router_inputs(512, 160, torch.float32, seed=s)] for s in range(3)]
+    # hidden 4104 (4096 vector columns + 8 scalar ones) and k = 20 (the block cascade): two launches
+    sets_c2 = [list(inputs.combine_inputs(64, 20, 4104, BF16, seed=s)) for s in range(3)]
+    eo2, ui2, w2 = [t.cuda() for t in sets_c2[0]]
+    out2 = torch.empty(64, 4104, dtype=BF16, device="cuda")
+    _replay_matches_eager([eo2, ui2, w2], [out2], lambda: native.token_combine_fwd(eo2, ui2, w2, out2), sets_c2)
+    sets_r =[[inputs.router_inputs(512, 160, torch.float32, seed=s)] for s in range(3)]
     lg = sets_r[0][0].cuda()
     tw, ti = torch.empty(512, 6, device="cuda"), torch.empty(512, 6, dtype=torch.int64, device="cuda")
     _replay_matches_eager([lg], [tw, ti], lambda: native.moe_router_fwd(lg, tw, ti, True), sets_r)
