@@ -146,7 +146,10 @@ int32_t launch_token_gather_fwd(const void* src, const int64_t* indices, void* d
                                 int64_t hidden_dim, int32_t dtype, void* stream);
 
 /* Weighted combine: combined[t] = sum_j weights[t,j] * expert_output[unpermute_index[t,j]],
- * products rounded to fp32 and added in j order, the sum rounded to dtype.
+ * products rounded to fp32 and summed in torch-CPU's order for (x.float() * w).sum(dim=1)
+ * (j order, in ATen's 16-step blocks beyond k = 16, on the leading 32 * floor(h / 32)
+ * columns; ATen's four-slot order on the rest; a row sum when hidden_dim == 1), the
+ * sum rounded to dtype. Two launches when hidden_dim is not a multiple of 32.
  * expert_output: [N, hidden_dim], unpermute_index: int64 [n_tokens, k], weights:
  * float32 [n_tokens, k], combined: [n_tokens, hidden_dim]. A negative index
  * drops its term.
@@ -167,10 +170,11 @@ int32_t launch_token_combine_checked_fwd(const void* expert_output, const int64_
                                          int64_t n_tokens, int64_t k, int64_t hidden_dim, int32_t dtype,
                                          void* stream);
 
-/* Softmax top-k router: per token, probs = softmax(float(logits)); the k largest
- * (descending; ties to the lower expert index) into topk_weights float32
+/* Softmax top-k router: per token, probs = softmax(float(logits)) in torch-CPU's
+ * float32 order on an AVX-512 host (SLEEF's expf, 16-lane sums, the reciprocal's
+ * product); the k largest (descending; ties to the lower expert index) into topk_weights float32
  * [num_tokens, k] and topk_indices int64 [num_tokens, k], renormalised to sum
- * to 1 when renormalize != 0. num_experts <= 256 and k <= num_experts, else
+ * to 1 when renormalize != 0 (ATen's row-sum order, an IEEE division). num_experts <= 256 and k <= num_experts, else
  * hipErrorInvalidValue.
  * Replaces reference csrc/includes/moe_router.h:20-29. */
 int32_t launch_moe_router_fwd(const void* logits, float* topk_weights, int64_t* topk_indices,
