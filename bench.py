@@ -315,6 +315,15 @@ def _ops(torch, native):
 
     ops.append(Op("moe_router", "moe_router_f32_2048x160_top6", rt * re_ * 4 + rt * rk * 12, mkr,
                   lambda b: native.moe_router_fwd(b["lg"], b["w"], b["i"], True), rt * re_ * 4, [rt, re_, rk]))
+    # The reference benchmark's Mixtral-shaped case (benchmarks/moe_router_bench.py:40): one lane per token.
+    mt, me, mk = 4096, 8, 2
+
+    def mkr8():
+        return dict(lg=rn(mt, me, dtype=torch.float32), w=torch.empty(mt, mk, device=dev),
+                    i=torch.empty(mt, mk, dtype=torch.int64, device=dev))
+
+    ops.append(Op("moe_router_e8", "moe_router_f32_4096x8_top2", mt * me * 4 + mt * mk * 12, mkr8,
+                  lambda b: native.moe_router_fwd(b["lg"], b["w"], b["i"], True), mt * me * 4, [mt, me, mk]))
 
     # The index bookkeeping between them (compute_permutation with num_experts):
     # the router's [2048, 6] expert ids in, permute / unpermute int64 out.

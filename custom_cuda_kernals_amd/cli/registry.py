@@ -323,12 +323,14 @@ REGISTRY: dict[str, OpSpec] = {
             formula="probs = softmax(float(logits)); top-k descending, ties to the lower index; w / sum(w)",
             dtypes=("float32", "float16", "bfloat16"),
             memory_profile="latency-bound (1.3 MB at 2048 x 160).",
-            design=("one wave per token, 4 experts per lane; wave arg-max per selection",),
-            target="indices equal the oracle's (exact ties aside), weights within 1e-5",
+            design=("E <= 8: one lane per token, every step serial in its registers",
+                    "9..32 experts (up to 64 from 4096 tokens): four lanes per token over 16-expert stripes",
+                    "otherwise one wave per token, 4 experts per lane; wave arg-max per selection"),
+            target="weights bit-exact against torch-CPU; indices equal the oracle's (exact ties aside)",
             reference=("baselines/moe_router.py:117-128", "csrc/kernels/moe_router.cu",
                        "csrc/includes/moe_router.h:20-29"),
             python_api=("moe_router",), c_entry_points=("launch_moe_router_fwd",), sources=(_CSRC + "moe_router.hip",),
-            test_files=("tests/test_moe_router_gpu.py", "tests/test_oracle_moe.py"), bench_ops=("moe_router",),
+            test_files=("tests/test_moe_router_gpu.py", "tests/test_oracle_moe.py"), bench_ops=("moe_router", "moe_router_e8"),
             build_target=_t_moe_router),
     ]
 }

@@ -18,7 +18,13 @@
 // Ties between equal probabilities go to the lower expert index (torch's
 // topk orders exact ties its own way).
 //
-// Design: one wave64 per token, up to 256 experts (4 per lane, expert
+// Three forms, by expert count E (and token count T), the same steps and
+// results in each:
+//   * E <= 8: one lane per token (moe_router_lanes);
+//   * 9 <= E <= 32, and E <= 64 from T = 4096 on: four lanes per token, each
+//     holding its quarter of every 16-expert stripe (moe_router_groups);
+//   * otherwise one wave per token (moe_router_waves), below.
+// One wave64 per token holds up to 256 experts (4 per lane, expert
 // e = lane + 64 * slot). The max is a wave all-reduction (DPP). The
 // exponentials go to a per-wave LDS row; every lane then runs its lane
 // class's ordered sum (lanes 16-63 repeat lanes 0-15), and the xor tree is
@@ -66,32 +72,34 @@ __device__ inline float softmax_sum_avx512(const float* e, int n, int lane) {
   return bits_f32((uint32_t)__builtin_amdgcn_readfirstlane((int)f32_bits(acc)));
 }
 
-// ATen's float32 row sum of n < 512 non-negative addends, serially
-// (wave-uniform): 8-lane vectors in 4 slots, each slot one running sum from
-// zero (no 16-step block of a slot completes below 512 addends, so the
-// cascade's other levels stay zero), the leftover vectors into slot 0, then
-// the trailing scalars and the 8 lanes in order; rows under 8 addends as
-// scalars in 4 slots. Adding the zero levels (or a leading zero) changes no
-// non-negative sum, so they are left out.
+// ATen's float32 row sum of n < 512 non-negative addends v[0], v[STRIDE],
+// v[2 * STRIDE], ..., serially: 8-lane vectors in 4 slots, each slot one
+// running sum from zero (no 16-step block of a slot completes below 512
+// addends, so the cascade's other levels stay zero), the leftover vectors
+// into slot 0, then the trailing scalars and the 8 lanes in order; rows under
+// 8 addends as scalars in 4 slots. Adding the zero levels (or a leading zero)
+// changes no non-negative sum, so they are left out.
+template <int STRIDE>
 __device__ inline float aten_small_row_sum(const float* v, int n) {
   if (n < 8) {
     const int s = n >> 2;
-    float p0 = s ? v[0] : 0.0f, p1 = s ? v[1] : 0.0f, p2 = s ? v[2] : 0.0f, p3 = s ? v[3] : 0.0f;
-    for (int u = 4 * s; u < n; ++u) p0 = p0 + v[u];
+    float p0 = s ? v[0] : 0.0f, p1 = s ? v[STRIDE] : 0.0f, p2 = s ? v[2 * STRIDE] : 0.0f,
+          p3 = s ? v[3 * STRIDE] : 0.0f;
+    for (int u = 4 * s; u < n; ++u) p0 = p0 + v[u * STRIDE];
     return ((p0 + p1) + p2) + p3;
   }
   const int nv = n >> 3, s = nv >> 2;
   float total = 0.0f;
-  for (int e = nv * 8; e < n; ++e) total = total + v[e];
+  for (int e = nv * 8; e < n; ++e) total = total + v[e * STRIDE];
   for (int l = 0; l < 8; ++l) {
     float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
     for (int i = 0; i < s; ++i) {
-      p0 = p0 + v[(4 * i + 0) * 8 + l];
-      p1 = p1 + v[(4 * i + 1) * 8 + l];
-      p2 = p2 + v[(4 * i + 2) * 8 + l];
-      p3 = p3 + v[(4 * i + 3) * 8 + l];
+      p0 = p0 + v[((4 * i + 0) * 8 + l) * STRIDE];
+      p1 = p1 + v[((4 * i + 1) * 8 + l) * STRIDE];
+      p2 = p2 + v[((4 * i + 2) * 8 + l) * STRIDE];
+      p3 = p3 + v[((4 * i + 3) * 8 + l) * STRIDE];
     }
-    for (int vec = 4 * s; vec < nv; ++vec) p0 = p0 + v[vec * 8 + l];
+    for (int vec = 4 * s; vec < nv; ++vec) p0 = p0 + v[(vec * 8 + l) * STRIDE];
     total = total + (((p0 + p1) + p2) + p3);
   }
   return total;
@@ -178,7 +186,7 @@ __global__ __launch_bounds__(256) void moe_router_waves(const void* __restrict__
     float wsum = 1.0f;
     if (renormalize) {
       __builtin_amdgcn_wave_barrier();
-      wsum = aten_small_row_sum(row, k);
+      wsum = aten_small_row_sum<1>(row, k);
     }
 #pragma unroll
     for (int s = 0; s < kSlots; ++s) {
@@ -191,10 +199,309 @@ __global__ __launch_bounds__(256) void moe_router_waves(const void* __restrict__
   }
 }
 
+// One lane per token, for up to EMAX <= 8 experts: the same steps as
+// moe_router_waves, each done serially in the lane's registers (the max over
+// the row, the exponentials and their sum in index order, the k arg-max
+// rounds over a live-expert mask with the lower index kept on ties). A wave
+// holds 64 consecutive tokens, whose rows are contiguous, so VEC's 16-byte
+// row loads are coalesced across the wave. The selected weights go to LDS in
+// [round][thread] order (no bank conflicts, no barrier: each thread reads
+// back only its own column) for the renormalising sum.
+constexpr int kLaneThreads = 64;
+constexpr int kLaneMaxExperts = 8;
+
+template <class C, int EMAX, bool VEC>
+__global__ __launch_bounds__(kLaneThreads) void moe_router_lanes(const void* __restrict__ logits,
+                                                                 float* __restrict__ topk_w,
+                                                                 int64_t* __restrict__ topk_i, int64_t n_tokens,
+                                                                 int n_experts, int k, int renormalize) {
+  static_assert(EMAX <= kLaneMaxExperts && EMAX < kSoftmaxLanes && (!VEC || EMAX % C::VEC == 0),
+                "lane router shape");
+  __shared__ float sel[EMAX][kLaneThreads];
+  const int tid = threadIdx.x;
+  const int64_t t = (int64_t)blockIdx.x * kLaneThreads + tid;
+  if (t >= n_tokens) return;  // nothing below synchronises
+  const int n = n_experts;
+  float x[EMAX];
+  if constexpr (VEC) {
+    // n is a multiple of C::VEC and the rows are 16-byte aligned.
+    const u32x4* r = reinterpret_cast<const u32x4*>(static_cast<const char*>(logits) + t * n * C::kBytes);
+#pragma unroll
+    for (int v = 0; v < EMAX / C::VEC; ++v) {
+      float f[C::VEC];
+      if (v * C::VEC < n) {
+        C::unpack(__builtin_nontemporal_load(r + v), f);
+      } else {
+#pragma unroll
+        for (int j = 0; j < C::VEC; ++j) f[j] = -__builtin_inff();
+      }
+#pragma unroll
+      for (int j = 0; j < C::VEC; ++j) x[v * C::VEC + j] = f[j];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) x[e] = e < n ? C::load1(logits, t * n + e) : -__builtin_inff();
+  }
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) m = __builtin_elementwise_maximum(m, x[e]);
+  float p[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) p[e] = e < n ? SleefExpf::eval_ldexp(x[e] - m) : 0.0f;
+  float total = p[0];
+#pragma unroll
+  for (int e = 1; e < EMAX; ++e) {
+    if (e < n) total = total + p[e];
+  }
+  const float inv = 1.0f / total;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) p[e] = p[e] * inv;
+
+  uint32_t live = (1u << n) - 1u;
+  for (int i = 0; i < k; ++i) {
+    int32_t key = -1;
+    uint32_t best = 0xffffffffu;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+      const int32_t b = (int32_t)f32_bits(p[e]);
+      if (((live >> e) & 1u) && b > key) {
+        key = b;
+        best = (uint32_t)e;
+      }
+    }
+    if (best < (uint32_t)EMAX) live &= ~(1u << best);
+    sel[i][tid] = bits_f32((uint32_t)key);
+    topk_i[t * k + i] = (int64_t)best;
+  }
+  const float wsum = renormalize ? aten_small_row_sum<kLaneThreads>(&sel[0][tid], k) : 1.0f;
+  for (int i = 0; i < k; ++i) topk_w[t * k + i] = renormalize ? sel[i][tid] / wsum : sel[i][tid];
+}
+
+// G lanes per token (G = 2 or 4), for n <= 16 * NS experts. The row is
+// cut into stripes of 16 experts (the AVX-512 vector), and lane r of a group
+// holds the CW = 16 / G experts [16 s + r CW, 16 s + (r + 1) CW) of every
+// stripe s, so each of the 16 lane classes of the softmax sum lives in one
+// lane, in stripe order. The xor tree's steps 8, 4, 2, 1 pair class L with
+// L ^ step: across lanes (a DPP exchange with the lane r ^ (step / CW)) while
+// step >= CW, in the lane's registers below. Every lane computes the tree
+// for its own classes; floating-point addition is commutative, so after the
+// cross-lane steps the lanes of a group hold the same values and all end
+// with class 0's total. Below 16 experts (one stripe) the sum is a running
+// sum handed from lane to lane instead. The max and each top-k round's arg-max are group
+// all-reductions (xor 1 and xor 2 quad permutations). Lane r of a group
+// writes the outputs of the rounds i = r mod G.
+constexpr int kDppRowShr1 = 0x111;     // lane i reads lane i - 1 of its row
+constexpr int kDppQuadBcast3 = 0xFF;  // quad_perm:[3,3,3,3]
+constexpr int kDppQuadBcast1 = 0xF5;  // quad_perm:[1,1,3,3]
+
+template <int G, class Op>
+__device__ inline uint32_t group_allreduce(uint32_t v, Op op) {
+  static_assert(G == 2 || G == 4, "group size");
+  v = op(v, dpp<kDppQuadXor1>(v));
+  if constexpr (G == 4) v = op(v, dpp<kDppQuadXor2>(v));
+  return v;
+}
+
+// VB: bytes per row load, 16 (whole 16-byte vectors of a chunk), 8 (a
+// chunk of four 2-byte experts) or 0 (one element at a time).
+template <class C, int G, int NS, int VB>
+__global__ __launch_bounds__(kLaneThreads) void moe_router_groups(const void* __restrict__ logits,
+                                                                  float* __restrict__ topk_w,
+                                                                  int64_t* __restrict__ topk_i, int64_t n_tokens,
+                                                                  int n_experts, int k, int renormalize) {
+  constexpr int CW = kSoftmaxLanes / G;  // experts of one stripe per lane
+  constexpr int PER = NS * CW;           // experts per lane
+  constexpr int TPB = kLaneThreads / G;  // tokens per workgroup
+  static_assert(PER <= 32 && (VB != 16 || CW % C::VEC == 0) && (VB != 8 || CW * C::kBytes == 8),
+                "group router shape");
+  __shared__ float sel[NS * kSoftmaxLanes][TPB];
+  const int tid = threadIdx.x, r = tid % G, slot = tid / G;
+  const int64_t t = (int64_t)blockIdx.x * TPB + slot;
+  if (t >= n_tokens) return;  // whole groups leave together; nothing below synchronises
+  const int n = n_experts;
+  float x[PER];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int e0 = kSoftmaxLanes * s + r * CW;
+    if constexpr (VB == 8) {
+      // n is a multiple of 4 and the rows are 8-byte aligned.
+      float f[C::VEC];
+      if (e0 < n) {
+        const u32x2 w = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x2*>(static_cast<const char*>(logits) + (t * n + e0) * C::kBytes));
+        C::unpack((u32x4){w.x, w.y, 0u, 0u}, f);
+      } else {
+#pragma unroll
+        for (int j = 0; j < CW; ++j) f[j] = -__builtin_inff();
+      }
+#pragma unroll
+      for (int j = 0; j < CW; ++j) x[s * CW + j] = f[j];
+    } else if constexpr (VB == 16) {
+      // n is a multiple of C::VEC and the rows are 16-byte aligned.
+      const u32x4* v = reinterpret_cast<const u32x4*>(static_cast<const char*>(logits) + (t * n + e0) * C::kBytes);
+#pragma unroll
+      for (int q = 0; q < CW / C::VEC; ++q) {
+        float f[C::VEC];
+        if (e0 + q * C::VEC < n) {
+          C::unpack(__builtin_nontemporal_load(v + q), f);
+        } else {
+#pragma unroll
+          for (int j = 0; j < C::VEC; ++j) f[j] = -__builtin_inff();
+        }
+#pragma unroll
+        for (int j = 0; j < C::VEC; ++j) x[s * CW + q * C::VEC + j] = f[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < CW; ++j) x[s * CW + j] = e0 + j < n ? C::load1(logits, t * n + e0 + j) : -__builtin_inff();
+    }
+  }
+  float mloc = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < PER; ++i) mloc = __builtin_elementwise_maximum(mloc, x[i]);
+  const float m = bits_f32(group_allreduce<G>(f32_bits(mloc), MaxF32{}));
+  float p[PER];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+#pragma unroll
+    for (int j = 0; j < CW; ++j) {
+      const int e = kSoftmaxLanes * s + r * CW + j;
+      p[s * CW + j] = e < n ? SleefExpf::eval_ldexp(x[s * CW + j] - m) : 0.0f;
+    }
+  }
+  float total;
+  if (NS == 1 && n < kSoftmaxLanes) {
+    // e_0 + e_1 + ... in order: lane 0 starts the running sum, and each lane
+    // in turn takes it from the lane below (row_shr:1) and adds its own
+    // experts; the last lane's sum goes to the whole group.
+    float run = p[0];
+#pragma unroll
+    for (int j = 1; j < CW; ++j) {
+      if (j < n) run = run + p[j];
+    }
+#pragma unroll
+    for (int g = 1; g < G; ++g) {
+      const float below = bits_f32(dpp<kDppRowShr1>(f32_bits(run)));
+      if (r == g) {
+        run = below;
+#pragma unroll
+        for (int j = 0; j < CW; ++j) {
+          if (g * CW + j < n) run = run + p[j];
+        }
+      }
+    }
+    total = bits_f32(dpp<G == 4 ? kDppQuadBcast3 : kDppQuadBcast1>(f32_bits(run)));
+  } else {
+    // Lane classes r CW + j: stripe 0 is whole (n >= 16), the others add in order.
+    float acc[CW];
+#pragma unroll
+    for (int j = 0; j < CW; ++j) acc[j] = p[j];
+#pragma unroll
+    for (int s = 1; s < NS; ++s) {
+#pragma unroll
+      for (int j = 0; j < CW; ++j) {
+        if (kSoftmaxLanes * s + r * CW + j < n) acc[j] = acc[j] + p[s * CW + j];
+      }
+    }
+#pragma unroll
+    for (int step = kSoftmaxLanes / 2; step >= CW; step >>= 1) {
+#pragma unroll
+      for (int j = 0; j < CW; ++j) {
+        const uint32_t o =
+            step / CW == 1 ? dpp<kDppQuadXor1>(f32_bits(acc[j])) : dpp<kDppQuadXor2>(f32_bits(acc[j]));
+        acc[j] = acc[j] + bits_f32(o);
+      }
+    }
+#pragma unroll
+    for (int step = CW / 2; step > 0; step >>= 1) {
+#pragma unroll
+      for (int j = 0; j < step; ++j) acc[j] = acc[j] + acc[j + step];
+    }
+    total = acc[0];
+  }
+  const float inv = 1.0f / total;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) p[i] = p[i] * inv;
+
+  uint32_t live = 0u;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+#pragma unroll
+    for (int j = 0; j < CW; ++j) {
+      if (kSoftmaxLanes * s + r * CW + j < n) live |= 1u << (s * CW + j);
+    }
+  }
+  for (int i = 0; i < k; ++i) {
+    int32_t key = -1;
+    uint32_t mine = 0xffffffffu;
+    int bit = -1;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+#pragma unroll
+      for (int j = 0; j < CW; ++j) {
+        const int32_t b = (int32_t)f32_bits(p[s * CW + j]);
+        if (((live >> (s * CW + j)) & 1u) && b > key) {
+          key = b;
+          mine = (uint32_t)(kSoftmaxLanes * s + r * CW + j);
+          bit = s * CW + j;
+        }
+      }
+    }
+    const uint32_t best = group_allreduce<G>((uint32_t)key, MaxI32{});
+    const uint32_t pick = group_allreduce<G>((int32_t)best == key ? mine : 0xffffffffu, MinU32{});
+    if (pick == mine && bit >= 0) live &= ~(1u << bit);
+    sel[i][slot] = bits_f32(best);
+    if (i % G == r) topk_i[t * k + i] = (int64_t)pick;
+  }
+  const float wsum = renormalize ? aten_small_row_sum<TPB>(&sel[0][slot], k) : 1.0f;
+  for (int i = r; i < k; i += G) topk_w[t * k + i] = renormalize ? sel[i][slot] / wsum : sel[i][slot];
+}
+
 }  // namespace
 }  // namespace cck
 
 using namespace cck;
+
+namespace {
+
+template <class C, int EMAX>
+void launch_router_lanes(const void* logits, float* w, int64_t* idx, int64_t t, int n, int k, int renorm,
+                         hipStream_t st) {
+  const unsigned grid = (unsigned)((t + kLaneThreads - 1) / kLaneThreads);
+  const bool vec = n % C::VEC == 0 && (reinterpret_cast<uintptr_t>(logits) & 15u) == 0;
+  if (vec) {
+    moe_router_lanes<C, EMAX, true><<<grid, kLaneThreads, 0, st>>>(logits, w, idx, t, n, k, renorm);
+  } else {
+    moe_router_lanes<C, EMAX, false><<<grid, kLaneThreads, 0, st>>>(logits, w, idx, t, n, k, renorm);
+  }
+}
+
+template <class C, int G, int NS>
+void launch_router_groups(const void* logits, float* w, int64_t* idx, int64_t t, int n, int k, int renorm,
+                          hipStream_t st) {
+  constexpr int TPB = kLaneThreads / G, CW = kSoftmaxLanes / G;
+  const unsigned grid = (unsigned)((t + TPB - 1) / TPB);
+  const uintptr_t a = reinterpret_cast<uintptr_t>(logits);
+  if constexpr (CW % C::VEC == 0) {
+    if (n % C::VEC == 0 && (a & 15u) == 0) {
+      moe_router_groups<C, G, NS, 16><<<grid, kLaneThreads, 0, st>>>(logits, w, idx, t, n, k, renorm);
+      return;
+    }
+  } else if constexpr (CW * C::kBytes == 8) {
+    if (n % CW == 0 && (a & 7u) == 0) {
+      moe_router_groups<C, G, NS, 8><<<grid, kLaneThreads, 0, st>>>(logits, w, idx, t, n, k, renorm);
+      return;
+    }
+  }
+  moe_router_groups<C, G, NS, 0><<<grid, kLaneThreads, 0, st>>>(logits, w, idx, t, n, k, renorm);
+}
+
+// Group kernels serve up to 64 experts; from 33 on only with enough tokens,
+// where the wave kernel's one wave per token no longer fits the GPU at once.
+constexpr int kGroupMaxExperts = 64;
+constexpr int64_t kGroupWideMinTokens = 4096;
+
+}  // namespace
 
 extern "C" int32_t launch_moe_router_fwd(const void* logits, float* topk_weights, int64_t* topk_indices,
                                          int64_t num_tokens, int64_t num_experts, int64_t k, int32_t dtype,
@@ -203,10 +510,28 @@ extern "C" int32_t launch_moe_router_fwd(const void* logits, float* topk_weights
   if (num_experts > kMaxExperts || k > num_experts || k < 0) return (int32_t)hipErrorInvalidValue;
   if (k == 0) return (int32_t)hipSuccess;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int n = (int)num_experts, kk = (int)k, rn = renormalize != 0;
+  // One workgroup per 64 / G tokens: every grid below fits for any token count this guard lets through.
+  const bool small_grid = num_tokens <= (int64_t)kLaneThreads * (INT32_MAX / 4);
+  const bool groups = n <= 2 * kSoftmaxLanes || (n <= kGroupMaxExperts && num_tokens >= kGroupWideMinTokens);
   return with_codec(dtype, [&](auto codec) {
     using C = decltype(codec);
+    if (small_grid && n <= kLaneMaxExperts) {
+      launch_router_lanes<C, kLaneMaxExperts>(logits, topk_weights, topk_indices, num_tokens, n, kk, rn, st);
+      return launch_status();
+    }
+    if (small_grid && groups) {
+      if (n <= kSoftmaxLanes) {
+        launch_router_groups<C, 4, 1>(logits, topk_weights, topk_indices, num_tokens, n, kk, rn, st);
+      } else if (n <= 2 * kSoftmaxLanes) {
+        launch_router_groups<C, 4, 2>(logits, topk_weights, topk_indices, num_tokens, n, kk, rn, st);
+      } else {
+        launch_router_groups<C, 4, 4>(logits, topk_weights, topk_indices, num_tokens, n, kk, rn, st);
+      }
+      return launch_status();
+    }
     moe_router_waves<C><<<flat_grid(num_tokens, kWavesPerGroup, kMaxRowGroups), 256, 0, st>>>(
-        logits, topk_weights, topk_indices, num_tokens, (int)num_experts, (int)k, renormalize != 0);
+        logits, topk_weights, topk_indices, num_tokens, n, kk, rn);
     return launch_status();
   });
 }

@@ -11,6 +11,12 @@ through the oracle's probabilities: the probability of each selected expert
 must equal the oracle's top-k at that position, bit for bit, so a different
 expert is accepted only at an exact tie (torch's topk orders those its own
 way; the kernel takes the lower expert index).
+
+Up to 8 experts one lane holds a token; a group of four lanes (16-expert
+stripes) holds one of 9 to 32 experts, and of up to 64 from 4096 tokens on;
+otherwise a wave does: the cases cover each form's edges (expert counts
+around 8, 16, 32 and 64, k = E, token counts that leave a partial workgroup
+or cross 4096) and rows that are not 16-byte aligned.
 """
 
 from __future__ import annotations
@@ -26,7 +32,12 @@ pytestmark = pytest.mark.gpu
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
 CASES = [(2048, 8, 2, True), (2048, 160, 6, True), (1024, 32, 1, True), (1024, 32, 2, True), (1024, 32, 4, True),
          (1024, 32, 8, True), (256, 100, 4, True), (257, 16, 2, True), (64, 1, 1, True), (64, 8, 8, True),
-         (128, 256, 8, True), (256, 16, 2, False), (1, 16, 2, True), (0, 16, 2, True), (96, 256, 256, True)]
+         (128, 256, 8, True), (256, 16, 2, False), (1, 16, 2, True), (0, 16, 2, True), (96, 256, 256, True),
+         (5, 9, 3, True), (100, 12, 12, True), (333, 17, 3, True), (65, 24, 5, False), (130, 31, 31, True),
+         (3, 33, 33, False), (77, 48, 7, True), (50, 64, 64, True), (129, 65, 9, True), (31, 127, 5, True),
+         (97, 128, 16, True), (40, 129, 8, True), (4100, 8, 2, True), (1000, 32, 8, False), (4095, 48, 6, True),
+         (4096, 48, 6, True), (4101, 64, 64, False), (4097, 33, 5, True), (33, 5, 5, True), (70, 3, 2, False),
+         (200, 13, 4, False), (64, 15, 15, True), (129, 10, 1, True)]
 
 
 def _check(logits, k, renorm):
@@ -63,6 +74,39 @@ def test_router_exact_ties_pick_lower_index():
     w, i = moe_router(logits.cuda(), 4)
     assert torch.equal(i.cpu()[:, :3], torch.tensor([[3, 5, 9]] * 8))
     assert bool((i.cpu()[:, 3] == 0).all())  # next: the lowest of the equal zeros
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("e", [8, 12, 16, 32, 64, 128])
+def test_router_unaligned_rows(e, dtype):
+    """Logits one element past a 16-byte boundary: the kernels take element loads."""
+    t, k = 4100, min(e, 6)
+    logits = inputs.router_inputs(t, e, dtype, seed=e)
+    flat = torch.empty(t * e + 1, dtype=dtype, device="cuda")
+    dev = flat[1:].view(t, e)
+    dev.copy_(logits.cuda())
+    assert dev.data_ptr() % 16 != 0
+    w, i = moe_router(dev, k)
+    w_ref, _ = moe.moe_router_avx512(logits, k)
+    assert torch.equal(w.cpu().view(torch.int32), w_ref.view(torch.int32))
+    p = moe.softmax_probs(logits)
+    assert torch.equal(torch.gather(p, 1, i.cpu()), torch.gather(p, 1, torch.topk(p, k).indices))
+
+
+@pytest.mark.parametrize("e", [12, 32, 100])
+def test_router_ties_across_lanes_and_minus_inf(e):
+    """Equal maxima held by different lanes of a token's group, and -inf
+    logits (probability +0, picked last, lowest index first)."""
+    logits = torch.full((9, e), -float("inf"))
+    picks = [1, e // 2 - 1, e // 2 + 3, e - 2]
+    logits[:, picks] = 1.5
+    logits[:, 0] = 0.25
+    w, i = moe_router(logits.cuda(), 6)
+    i = i.cpu()
+    assert torch.equal(i[:, :5], torch.tensor([picks + [0]] * 9))
+    assert bool((i[:, 5] == 2).all())  # the lowest index among the +0 probabilities
+    w_ref, _ = moe.moe_router_avx512(logits, 6)
+    assert torch.equal(w.cpu().view(torch.int32), w_ref.view(torch.int32))
 
 
 def test_router_rejections():
