@@ -89,6 +89,38 @@ __global__ __launch_bounds__(THREADS) void token_gather_rows(const u32x4* __rest
   }
 }
 
+// token_gather_rows on a grid that the GPU holds at once: each workgroup
+// loops over its groups of R rows and loads the next group's R indices while
+// the current rows are in flight, so only the first group waits for its
+// indices before its row loads.
+template <int THREADS, int R>
+__global__ __launch_bounds__(THREADS) void token_gather_rows_pf(const u32x4* __restrict__ src,
+                                                                const int64_t* __restrict__ idx,
+                                                                u32x4* __restrict__ dst, int64_t n_dst,
+                                                                int64_t row_vecs, int64_t n_src) {
+  const int64_t t = threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * R;
+  int64_t row0 = (int64_t)blockIdx.x * R;
+  int64_t s[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) s[r] = row0 + r < n_dst ? idx[row0 + r] : -1;  // uniform: scalar loads
+  for (; row0 < n_dst; row0 += stride) {
+    u32x4 v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      v[r] = (u32x4){0u, 0u, 0u, 0u};
+      if (s[r] >= 0 && s[r] < n_src && t < row_vecs) v[r] = ld_stream(src + s[r] * row_vecs + t);
+    }
+    const int64_t next = row0 + stride;
+#pragma unroll
+    for (int r = 0; r < R; ++r) s[r] = next + r < n_dst ? idx[next + r] : -1;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (row0 + r < n_dst && t < row_vecs) st_stream(v[r], dst + (row0 + r) * row_vecs + t);
+    }
+  }
+}
+
 // Any row length / alignment: element-wise (E = 1-, 2- or 4-byte element).
 template <class E>
 __global__ __launch_bounds__(256) void token_gather_elems(const E* __restrict__ src,
@@ -343,6 +375,13 @@ inline int32_t elem_bytes(int32_t dtype) {
   }
 }
 
+// Destination rows from which the short-row gather takes 8 rows per
+// workgroup step instead of 4: same-run A/B on MI355X, bf16 rows of 8 KB,
+// 11.5 vs 12.5 us at 2048 -> 4096 rows and 4096 -> 4096, 47.3 vs 48.6 us at
+// 16384 rows, 191.3 vs 194.7 at 65536 (with the index prefetch below);
+// 1024 -> 2048 rows took 7.5 vs 6.9 us with 8 (a grid of 256 workgroups).
+constexpr int64_t kGatherR8Min = 4096;
+
 int32_t gather(const void* src, const int64_t* indices, void* dst, int64_t n_dst, int64_t h,
                int32_t dtype, int64_t n_src, hipStream_t st) {
   if (n_dst <= 0 || h <= 0) return (int32_t)hipSuccess;
@@ -353,18 +392,41 @@ int32_t gather(const void* src, const int64_t* indices, void* dst, int64_t n_dst
   if (row_bytes % 16 == 0 && host_aligned(src, 16) && host_aligned(dst, 16)) {
     const int64_t rv = row_bytes / 16;
     if (rv <= 512) {
-      // One vector per thread, up to 512 threads, four rows per workgroup:
-      // 12.3 vs 12.6 us for one row per workgroup at 2048 -> 4096 rows of
-      // 8 KB on MI355X (13.0-13.5 with 2-8 vectors per thread).
-      constexpr int R = 4;
-      const unsigned g4 = row_grid((n_dst + R - 1) / R);
-      with_row_threads<1, 512>(rv, [&](auto threads) {
-        constexpr int TH = decltype(threads)::value;
-        token_gather_rows<TH, R><<<g4, TH, 0, st>>>(static_cast<const u32x4*>(src), indices,
-                                                   static_cast<u32x4*>(dst), n_dst, rv, n_src);
-      });
-    } else {
+      // One vector per thread, up to 512 threads, R rows per workgroup step:
+      // with R = 4, 12.3 vs 12.6 us for one row per workgroup at 2048 -> 4096
+      // rows of 8 KB on MI355X (13.0-13.5 with 2-8 vectors per thread).
+      // When there are more groups of R rows than the GPU holds at once, a
+      // resident grid loops over them with the next indices prefetched
+      // (without the prefetch, 8 rows per step lost at 16384 rows: 50.7 us).
+      auto run = [&](auto rows) {
+        constexpr int R = decltype(rows)::value;
+        const unsigned groups = row_grid((n_dst + R - 1) / R);
+        with_row_threads<1, 512>(rv, [&](auto threads) {
+          constexpr int TH = decltype(threads)::value;
+          const int64_t res = resident_groups<token_gather_rows_pf<TH, R>>(TH);
+          if (res > 0 && res < (int64_t)groups) {
+            token_gather_rows_pf<TH, R><<<(unsigned)res, TH, 0, st>>>(static_cast<const u32x4*>(src), indices,
+                                                                      static_cast<u32x4*>(dst), n_dst, rv, n_src);
+          } else {
+            token_gather_rows<TH, R><<<groups, TH, 0, st>>>(static_cast<const u32x4*>(src), indices,
+                                                           static_cast<u32x4*>(dst), n_dst, rv, n_src);
+          }
+        });
+      };
+      if (n_dst >= kGatherR8Min) {
+        run(std::integral_constant<int, 8>{});
+      } else {
+        run(std::integral_constant<int, 4>{});
+      }
+    } else if (rv <= 1024) {
       token_gather_vec<512, 1><<<grid, 512, 0, st>>>(static_cast<const u32x4*>(src), indices,
+                                                    static_cast<u32x4*>(dst), n_dst, rv, n_src);
+    } else {
+      // Rows of more than two 512-vector passes keep four vectors per thread
+      // in flight: 61.9 vs 64.5 us at 2048 -> 4096 fp32 rows of 11008, 31.1 vs
+      // 31.8 in bf16 (one vector per thread stays ahead up to 1024 vectors:
+      // 148.2 vs 149.3-150.6 us at 32768 bf16 rows of 7168).
+      token_gather_vec<512, 4><<<grid, 512, 0, st>>>(static_cast<const u32x4*>(src), indices,
                                                     static_cast<u32x4*>(dst), n_dst, rv, n_src);
     }
   } else if (es == 4) {
