@@ -443,6 +443,7 @@ int32_t gather(const void* src, const int64_t* indices, void* dst, int64_t n_dst
 }
 
 constexpr int64_t kCombineWideTokens = 4096;
+constexpr int64_t kCombineFewTokens = 1024;
 
 int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, int64_t n_tokens,
                 int64_t k, int64_t h, int32_t dtype, int64_t n_rows, hipStream_t st) {
@@ -462,6 +463,23 @@ int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, 
         token_combine_vec<C, 512, V, 2, false><<<grid, 512, 0, st>>>(
             static_cast<const u32x4*>(eo), uidx, w, static_cast<u32x4*>(out), n_tokens, k, rv, n_rows, order.p_main);
       };
+      // Many tokens, rows of 512 to 2048 vectors (4096 to 16384 bf16):
+      // 512-thread workgroups holding the row in one pass, measured on MI355X
+      // (graph-replayed) against the shapes below: 35.0 vs 38.1 us at T=8192,
+      // k=2, hidden 4096 (fp16 34.8 vs 37.2, fp32 66.6 vs 71.5); 186.5 vs
+      // 194.3 at T=8192, k=8, hidden 7168; 412.7 vs 437.2 at hidden 16384 (but
+      // 27.2 vs 26.3 at T=4096, k=8, hidden 2048, and 159.5 vs 158.5 at
+      // T=16384, k=6, hidden 4096).
+      const bool many = n_tokens >= kCombineWideTokens && (k <= 2 ? mv >= 512 : mv > 512) && mv <= 4 * 512;
+      // Few tokens, so few workgroups, and rows of 512 vectors or more: the
+      // same form, now for the loads it keeps in flight. Same-run A/B against
+      // the shapes below: bf16 hidden 4096 top-2 at 512 tokens 4.2 vs 5.7 us,
+      // top-6 at 256 6.1 vs 8.9, hidden 7168 top-6 at 512 11.6 vs 17.1; fp32
+      // hidden 4096 top-6 at 256 6.9 vs 14.9, top-2 at 1024 9.9 vs 11.5. From
+      // 1536 tokens it ties or loses (8.3 vs 7.9 us at bf16 hidden 4096, top 2),
+      // and shorter rows lose (6.1 vs 5.3 us at 512 tokens, hidden 2048 bf16,
+      // top 6).
+      const bool few = n_tokens <= kCombineFewTokens && k <= 16 && mv >= 512;
       if (mv == 0) {
         // Rows of 8 to 31 elements: scalar columns only.
       } else if (k > 16) {
@@ -471,14 +489,7 @@ int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, 
           token_combine_vec<C, TH, 1, 2, true><<<grid, TH, 0, st>>>(
               static_cast<const u32x4*>(eo), uidx, w, static_cast<u32x4*>(out), n_tokens, k, rv, n_rows, order.p_main);
         });
-      } else if (n_tokens >= kCombineWideTokens && (k <= 2 ? mv >= 512 : mv > 512) && mv <= 4 * 512) {
-        // Many tokens, rows of 512 to 2048 vectors (4096 to 16384 bf16):
-        // 512-thread workgroups holding the row in one pass, measured on
-        // MI355X (graph-replayed) against the shapes below: 35.0 vs 38.1 us at T=8192, k=2, hidden
-        // 4096 (fp16 34.8 vs 37.2, fp32 66.6 vs 71.5); 186.5 vs 194.3 at
-        // T=8192, k=8, hidden 7168; 412.7 vs 437.2 at hidden 16384 (but 10.4
-        // vs 9.2 at T=2048, k=2, hidden 4096, 27.2 vs 26.3 at T=4096, k=8,
-        // hidden 2048, and 159.5 vs 158.5 at T=16384, k=6, hidden 4096).
+      } else if (many || few) {
         if (mv <= 512) {
           wide(IntC<1>{});
         } else if (mv <= 1024) {
@@ -486,6 +497,17 @@ int32_t combine(const void* eo, const int64_t* uidx, const float* w, void* out, 
         } else {
           wide(IntC<4>{});
         }
+      } else if (k <= 2 && mv >= 1024) {
+        // Rows of 1024 vectors and more (fp32 hidden 4096, bf16 8192) in one
+        // pass of 256 threads: 12.8 vs 15.6 us at 1536 tokens, 17.6 vs 19.7 at
+        // 2048 (fp32 hidden 4096, top 2); 27.9 vs 30.0 at 3072 tokens (bf16
+        // hidden 8192); two passes of 128 threads for bf16 hidden 7168 stay
+        // faster (14.0 vs 15.3 us at 1536 tokens).
+        with_row_threads<4, 256>(mv, [&](auto threads) {
+          constexpr int TH = decltype(threads)::value;
+          token_combine_vec<C, TH, 4, 2, false><<<grid, TH, 0, st>>>(
+              static_cast<const u32x4*>(eo), uidx, w, static_cast<u32x4*>(out), n_tokens, k, rv, n_rows, order.p_main);
+        });
       } else if (k <= 2) {
         with_row_threads<4, 128>(mv, [&](auto threads) {
           constexpr int TH = decltype(threads)::value;

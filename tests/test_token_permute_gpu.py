@@ -28,7 +28,11 @@ DTYPES = [torch.float32, torch.float16, torch.bfloat16]
 GATHER_CASES = [(2048, 4096, 4096), (2048, 4096, 11008), (257, 513, 100), (1, 1, 256), (64, 0, 256),
                 (128, 256, 16)]
 COMBINE_CASES = [(2048, 2, 4096), (2048, 6, 4096), (256, 1, 512), (256, 8, 512), (257, 3, 100), (1, 2, 256),
-                 (0, 2, 256), (128, 4, 16)]
+                 (0, 2, 256), (128, 4, 16),
+                 # few tokens, rows of >= 512 vectors (one 512-thread pass, or two at fp32 hidden 16384); the
+                 # boundary at 1024 tokens and k = 16; one 256-thread pass of 1024-vector rows at top-1/2
+                 (512, 2, 4096), (300, 6, 7168), (100, 3, 16384), (1024, 16, 4096), (1025, 2, 4096),
+                 (1536, 2, 4096), (1100, 1, 8192)]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
