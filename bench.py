@@ -9,7 +9,13 @@ stream the kernels run on, after the --warmup eager launches and untimed
 replays of the graph for 0.15 s (GPU clocks ramp up under sustained load).
 Every launch of a timed run uses a different set of input/output buffers,
 rotating over enough sets that the working set is >= 2 GiB, so no step can be
-served from the 256 MB Infinity Cache left warm by the previous one.
+served from the 256 MB Infinity Cache left warm by the previous one. Where
+that takes more sets than --steps (ops whose set is under 2 GiB / steps), the
+graph launches the op once per set, up to 16384 sets, and the op's time is
+the replay's over that many launches, so the replays before the timed one
+leave none of its buffers on chip. The headline op and every BASELINE config
+op take exactly --steps launches (their sets are over 21 MB); only the small
+MoE ops take more.
 
 Each op also reports "per_call": the reference's own methodology (a cache
 flush before every call, HIP events around one call through the binding, so
@@ -44,6 +50,7 @@ if ROOT not in sys.path:
 
 PEAK_GBPS = 8000.0
 ROTATE_BYTES = 2 << 30
+MAX_SETS = 16384  # >= 512 MB of rotation down to 32 KB sets, twice the Infinity Cache
 WARM_S = 0.15
 
 
@@ -67,6 +74,10 @@ def _parse():
     p.add_argument("--markers", action="store_true",
                    help="wrap each op's timed graph replay in a ROCTx range named 'timed:<op>', so a "
                         "rocprofv3 --marker-trace --kernel-trace run can select exactly the timed dispatches")
+    p.add_argument("--suite", choices=["configs", "reference"], default="configs",
+                   help="reference: instead of the BASELINE configs, every case of the reference's own benchmark "
+                        "lists (benchmarks/*_bench.py) in its three dtypes; --ops then names families "
+                        "(rmsnorm_residual, swiglu, rope, fp8_quant, moe_router, token_gather, token_combine)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a 256 MiB device-to-device torch copy, the reference kernel "
                         "for scaling FETCH_SIZE / WRITE_SIZE counters")
@@ -338,8 +349,9 @@ def _ops(torch, native):
 
 
 def _time_op(torch, op, steps, warmup, use_graph=True, per_call=True):
-    nsets = max(2, math.ceil(ROTATE_BYTES / op.set_bytes))
+    nsets = min(MAX_SETS, max(2, math.ceil(ROTATE_BYTES / op.set_bytes)))
     sets = [op.make_set() for _ in range(nsets)]
+    launches = max(steps, nsets)
     torch.cuda.synchronize()
     for i in range(warmup):
         op.launch(sets[i % nsets])
@@ -363,7 +375,7 @@ def _time_op(torch, op, steps, warmup, use_graph=True, per_call=True):
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         with torch.cuda.graph(graph, stream=side):
-            for i in range(steps):
+            for i in range(launches):
                 op.launch(sets[i % nsets])
     torch.cuda.current_stream().wait_stream(side)
     graph.replay()  # untimed replay: first replay uploads the graph
@@ -388,7 +400,7 @@ def _time_op(torch, op, steps, warmup, use_graph=True, per_call=True):
     torch.cuda.synchronize()
     MARKERS.pop()
     ms = start.elapsed_time(end)
-    us = ms * 1000.0 / steps
+    us = ms * 1000.0 / launches
     gbps = op.nbytes / (us * 1e-6) / 1e9
     del graph
     per_call = _per_call_us(torch, op, sets) if per_call else None
@@ -396,7 +408,7 @@ def _time_op(torch, op, steps, warmup, use_graph=True, per_call=True):
     torch.cuda.empty_cache()
     return {"workload": op.workload, "shape": op.shape, "us": round(us, 3), "GB_per_s": round(gbps, 1),
             "frac_of_8TBps": round(gbps / PEAK_GBPS, 4), "algorithmic_bytes": op.nbytes,
-            "steps": steps, "buffer_sets": nsets, "total_ms": round(ms, 4), "per_call": per_call}
+            "steps": launches, "buffer_sets": nsets, "total_ms": round(ms, 4), "per_call": per_call}
 
 
 def _ceilings(torch, steps, warmup):
@@ -478,6 +490,156 @@ def _anchors(torch, steps, warmup):
     out["torch_compute_permutation"] = {"bounds": "moe_permutation", "us": r["us"], "GB_per_s": r["GB_per_s"],
                                         "frac_of_8TBps": r["frac_of_8TBps"], "bytes": t * k * 24}
     return out
+
+
+# Fractions of peak the reference publishes for a named case of its own
+# benchmarks (RTX 4070 Laptop GPU, 256 GB/s; project_plan.md:701-702, 726-733).
+REFERENCE_PUBLISHED = {("swiglu", "bs2_seq2048_d11008", "float16"): 0.855,
+                       ("rope", "batchsweep_16", "float16"): 0.831}
+
+
+def _reference_suite(torch, native):
+    """The reference's own benchmark case lists (benchmarks/{rmsnorm_residual,
+    swiglu,rope,fp8_quant,moe_router,token_permute}_bench.py), every case in
+    the three dtypes they run, through this library's launchers, with the
+    reference's bytes (`_ideal_bytes_moved`: weight and cos/sin tables left
+    out, FP8 scales left out, router outputs counted). Yields (family, case,
+    dtype name, Op)."""
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(0)
+    dts = (("float32", torch.float32), ("float16", torch.float16), ("bfloat16", torch.bfloat16))
+
+    def rn(shape, dt):
+        return torch.randn(shape, device=dev, dtype=torch.float32, generator=g).to(dt)
+
+    def op(name, nbytes, make, launch, set_bytes, shape):
+        return Op(name, name, nbytes, make, launch, set_bytes, shape)
+
+    sweep = [("seqsweep_128", 1, 128), ("seqsweep_512", 1, 512), ("seqsweep_2048", 1, 2048),
+             ("seqsweep_8192", 1, 8192), ("batchsweep_1", 1, 1024), ("batchsweep_4", 4, 1024),
+             ("batchsweep_16", 16, 1024)]
+    # rmsnorm_residual_bench.py:66-79
+    for case, b, s, h in [("bs4_seq128_h768", 4, 128, 768), ("bs2_seq2048_h4096", 2, 2048, 4096),
+                          ("bs1_seq4096_h4096", 1, 4096, 4096)] + [(c, b, s, 4096) for c, b, s in sweep]:
+        for dn, dt in dts:
+            es, rows = torch.tensor([], dtype=dt).element_size(), b * s
+            w = (1.0 + 0.1 * torch.randn(h, device=dev, generator=g)).to(dt)
+            yield "rmsnorm_residual", case, dn, op(
+                f"rmsnorm_residual/{case}/{dn}", rows * h * es * 4,
+                lambda rows=rows, h=h, dt=dt: dict(x=rn((rows, h), dt), r=rn((rows, h), dt),
+                                                   y=torch.empty(rows, h, dtype=dt, device=dev),
+                                                   ro=torch.empty(rows, h, dtype=dt, device=dev)),
+                lambda d, w=w: native.rmsnorm_residual_fwd(d["x"], d["r"], w, d["y"], d["ro"], 1e-5),
+                rows * h * es * 4, [rows, h])
+    # swiglu_bench.py:39-50
+    for case, b, s, d_ff in [("bs4_seq128_d3072", 4, 128, 3072), ("bs2_seq2048_d11008", 2, 2048, 11008),
+                             ("bs1_seq4096_d11008", 1, 4096, 11008)] + [(c, b, s, 11008) for c, b, s in sweep]:
+        for dn, dt in dts:
+            es, rows = torch.tensor([], dtype=dt).element_size(), b * s
+            yield "swiglu", case, dn, op(
+                f"swiglu/{case}/{dn}", rows * d_ff * es * 3,
+                lambda rows=rows, d_ff=d_ff, dt=dt: dict(g=rn((rows, d_ff), dt), u=rn((rows, d_ff), dt),
+                                                         y=torch.empty(rows, d_ff, dtype=dt, device=dev)),
+                lambda d: native.swiglu_fwd(d["g"], d["u"], d["y"]), rows * d_ff * es * 3, [rows, d_ff])
+    # rope_bench.py:39-50 (out of place, as the reference's rope(q, k, cos, sin) returns new tensors)
+    for case, b, s, hq, hkv, hd in [("bs4_seq128_mha", 4, 128, 12, 12, 64), ("bs2_seq2048_gqa", 2, 2048, 32, 8, 128),
+                                    ("bs1_seq4096_gqa", 1, 4096, 32, 8, 128)] + [(c, b, s, 32, 8, 128)
+                                                                                 for c, b, s in sweep]:
+        inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32, device=dev) / hd))
+        ang = torch.outer(torch.arange(s, dtype=torch.float32, device=dev), inv)
+        cos, sin = ang.cos().contiguous(), ang.sin().contiguous()
+        for dn, dt in dts:
+            es, elems = torch.tensor([], dtype=dt).element_size(), b * s * (hq + hkv) * hd
+            yield "rope", case, dn, op(
+                f"rope/{case}/{dn}", elems * es * 2,
+                lambda b=b, s=s, hq=hq, hkv=hkv, hd=hd, dt=dt: dict(
+                    q=rn((b, s, hq, hd), dt), k=rn((b, s, hkv, hd), dt),
+                    qo=torch.empty(b, s, hq, hd, dtype=dt, device=dev), ko=torch.empty(b, s, hkv, hd, dtype=dt, device=dev)),
+                lambda d, cos=cos, sin=sin: native.rope_fwd(d["q"], d["k"], cos, sin, d["qo"], d["ko"]),
+                elems * es * 2, [b, s, hq, hkv, hd])
+    # fp8_quant_bench.py:40-59: tensor (with the reference wrapper's zeroed int32) and 128 x 128 blocks
+    for case, m, n in [("small", 256, 256), ("medium", 1024, 1024), ("large", 4096, 4096), ("xlarge", 8192, 8192)]:
+        for dn, dt in dts:
+            es = torch.tensor([], dtype=dt).element_size()
+            for fmt in ("e4m3", "e5m2"):
+                f8 = torch.float8_e4m3fn if fmt == "e4m3" else torch.float8_e5m2
+
+                def mk(m=m, n=n, dt=dt, f8=f8):
+                    return dict(x=rn((m, n), dt), q=torch.empty(m, n, dtype=f8, device=dev),
+                                st=torch.empty(1, device=dev), amax=torch.zeros(1, dtype=torch.int32, device=dev),
+                                sb=torch.empty((m + 127) // 128, (n + 127) // 128, device=dev))
+
+                def tensor(d, fmt=fmt):
+                    d["amax"].zero_()
+                    native.fp8_quant_tensor_fwd(d["x"], d["q"], d["st"], d["amax"], fmt)
+
+                yield "fp8_quant", f"{case}_{fmt}_tensor", dn, op(f"fp8_quant/{case}_{fmt}_tensor/{dn}",
+                                                                 m * n * (es + 1), mk, tensor, m * n * (es + 1), [m, n])
+                yield "fp8_quant", f"{case}_{fmt}_block", dn, op(
+                    f"fp8_quant/{case}_{fmt}_block/{dn}", m * n * (es + 1), mk,
+                    lambda d, fmt=fmt: native.fp8_quant_block_fwd(d["x"], d["q"], d["sb"], fmt), m * n * (es + 1),
+                    [m, n])
+    # moe_router_bench.py:39-51
+    for case, t, e, k in [("mixtral_like", 4096, 8, 2), ("deepseek_like", 4096, 160, 6), ("ksweep_k1", 4096, 32, 1),
+                          ("ksweep_k2", 4096, 32, 2), ("ksweep_k4", 4096, 32, 4), ("ksweep_k8", 4096, 32, 8),
+                          ("tsweep_512", 512, 8, 2), ("tsweep_2048", 2048, 8, 2), ("tsweep_8192", 8192, 8, 2),
+                          ("tsweep_32768", 32768, 8, 2)]:
+        for dn, dt in dts:
+            es = torch.tensor([], dtype=dt).element_size()
+            yield "moe_router", case, dn, op(
+                f"moe_router/{case}/{dn}", t * e * es + t * k * 12,
+                lambda t=t, e=e, k=k, dt=dt: dict(lg=rn((t, e), dt), w=torch.empty(t, k, device=dev),
+                                                  i=torch.empty(t, k, dtype=torch.int64, device=dev)),
+                lambda d: native.moe_router_fwd(d["lg"], d["w"], d["i"], True), t * e * es + t * k * 12, [t, e, k])
+    # token_permute_bench.py:56-73
+    for case, ns, nd, h in [("mixtral_like", 2048, 4096, 4096), ("large_hidden", 2048, 4096, 11008),
+                            ("nsweep_1024", 1024, 1024, 4096), ("nsweep_4096", 4096, 4096, 4096),
+                            ("nsweep_16384", 16384, 16384, 4096), ("nsweep_65536", 65536, 65536, 4096)]:
+        for dn, dt in dts:
+            es = torch.tensor([], dtype=dt).element_size()
+            yield "token_gather", case, dn, op(
+                f"token_gather/{case}/{dn}", 2 * nd * h * es,
+                lambda ns=ns, nd=nd, h=h, dt=dt: dict(src=rn((ns, h), dt),
+                                                      idx=torch.randint(0, ns, (nd,), device=dev, generator=g),
+                                                      dst=torch.empty(nd, h, dtype=dt, device=dev)),
+                lambda d: native.token_gather_fwd(d["src"], d["idx"], d["dst"]), (ns + nd) * h * es, [ns, nd, h])
+    for case, t, k, h in [("mixtral_like", 2048, 2, 4096), ("deepseek_like", 2048, 6, 4096), ("tsweep_512", 512, 2, 4096),
+                          ("tsweep_2048", 2048, 2, 4096), ("tsweep_8192", 8192, 2, 4096),
+                          ("tsweep_32768", 32768, 2, 4096)]:
+        for dn, dt in dts:
+            es = torch.tensor([], dtype=dt).element_size()
+            yield "token_combine", case, dn, op(
+                f"token_combine/{case}/{dn}", (k + 1) * t * h * es,
+                lambda t=t, k=k, h=h, dt=dt: dict(
+                    eo=rn((t * k, h), dt), ui=torch.randperm(t * k, device=dev, generator=g).view(t, k),
+                    w=torch.rand(t, k, device=dev, generator=g), out=torch.empty(t, h, dtype=dt, device=dev)),
+                lambda d: native.token_combine_fwd(d["eo"], d["ui"], d["w"], d["out"]), (k + 1) * t * h * es,
+                [t, k, h])
+
+
+def _run_reference_suite(torch, native, args):
+    """Times every case of _reference_suite like the config ops (graph-replayed
+    kernel time over a >= 2 GiB rotation, plus the per-call time under the
+    reference's own method) and prints one table row per case to stderr and
+    one JSON line with all of them."""
+    wanted = None if args.ops == "all" else set(args.ops.split(","))
+    cases = []
+    print("# family | case | dtype | kernel us | of 8 TB/s | per-call us | reference published",
+          file=sys.stderr, flush=True)
+    for fam, case, dn, op in _reference_suite(torch, native):
+        if wanted and fam not in wanted:
+            continue
+        r = _time_op(torch, op, args.steps, args.warmup)
+        pub = REFERENCE_PUBLISHED.get((fam, case, dn))
+        row = {"family": fam, "case": case, "dtype": dn, "shape": op.shape, "bytes": op.nbytes, "us": r["us"],
+               "frac_of_8TBps": r["frac_of_8TBps"], "per_call_median_us": r["per_call"]["median_us"],
+               "reference_published_frac": pub}
+        cases.append(row)
+        print(f"# {fam} | {case} | {dn} | {r['us']:.2f} | {100 * r['frac_of_8TBps']:.1f} % | "
+              f"{r['per_call']['median_us']:.2f} | {'' if pub is None else f'{100 * pub:.1f} % of 256 GB/s'}",
+              file=sys.stderr, flush=True)
+    print(json.dumps({"suite": "reference", "metric": "achieved HBM bandwidth per case, reference bytes",
+                      "peak_GB_per_s": PEAK_GBPS, "steps": args.steps, "cases": cases}), flush=True)
 
 
 def _per_call_us(torch, op, sets, calls=30):
@@ -674,6 +836,9 @@ def main():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
 
+    if args.suite == "reference":
+        _run_reference_suite(torch, native, args)
+        return
     ops = _ops(torch, native)
     wanted = None if args.ops == "all" else set(args.ops.split(","))
     results = {}

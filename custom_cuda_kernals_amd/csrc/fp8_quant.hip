@@ -211,25 +211,32 @@ __global__ __launch_bounds__(THREADS * TW) void fp8_block_resident(const void* _
                         (uint32_t)(left < 0x7fffffff ? left : 0x7fffffff));
   u32x4 raw[ITEMS];
   uint32_t acc = 0;
+  // Loads without branches: an element outside the matrix reads the
+  // workgroup's first element (always inside it) and is replaced by zeros.
+  // Loading under a branch instead made the compiler copy the whole of raw[]
+  // at every join and wait on each load before the next: 232 VGPRs for fp32
+  // tiles (8 vectors per thread, one workgroup per CU), 111.2 vs 55.4 us at
+  // [8192, 8192] fp32, 6.29 vs 6.01 us at [2048, 4096] bf16 on MI355X.
+  const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int k = 0; k < ITEMS; ++k) {
     const int64_t row = row0 + k * RPP;
-    if (col_ok && row < m) {
-      if constexpr (RSRC) {
-        raw[k] = bx.ld16((uint32_t)(((int64_t)(rr + k * RPP) * n + tile * kTile + cv * C::VEC) * C::kBytes));
-      } else {
-        raw[k] = ld_stream(reinterpret_cast<const u32x4*>(static_cast<const char*>(x) + (row * n + col) * C::kBytes));
-      }
-      if constexpr (!SPLIT) acc = C::absmax_vec(raw[k], acc);
+    const bool ok = col_ok && row < m;
+    if constexpr (RSRC) {
+      const uint32_t off = (uint32_t)(((int64_t)(rr + k * RPP) * n + tile * kTile + cv * C::VEC) * C::kBytes);
+      raw[k] = bx.ld16(ok ? off : 0u);
+    } else {
+      raw[k] = ld_stream(
+          reinterpret_cast<const u32x4*>(static_cast<const char*>(x) + (ok ? row * n + col : origin) * C::kBytes));
     }
+    raw[k] = ok ? raw[k] : zero;
+    if constexpr (!SPLIT) acc = C::absmax_vec(raw[k], acc);
   }
   // SPLIT: every load is issued before the first max, instead of each max
   // waiting on its own load (see the launcher for when each pays).
   if constexpr (SPLIT) {
 #pragma unroll
-    for (int k = 0; k < ITEMS; ++k) {
-      if (col_ok && row0 + k * RPP < m) acc = C::absmax_vec(raw[k], acc);
-    }
+    for (int k = 0; k < ITEMS; ++k) acc = C::absmax_vec(raw[k], acc);
   }
   if constexpr (TW == 1) {
     acc = block_allreduce<NW>(acc, typename AmaxOp<C>::type{}, lds, 0);
