@@ -422,7 +422,11 @@ int32_t launch_rmsnorm(const void* x, const void* res, const void* w, void* y, u
   // for 1024 x 2; static 16384: 163.4 for 512 x 4 against 187.4).
   // fp32 rows stage their squares whole in LDS (aten_sum.hpp): up to
   // 1024 x 4 vectors (16384 elements, 64 KB of the 160 KB a gfx950
-  // workgroup may hold); longer ones loop.
+  // workgroup may hold); longer ones loop. Their plain-op shapes: 512 x 2
+  // for rows of 513-1024 vectors, 512 x 4 up to 2048 (same-run A/B on
+  // MI355X against 1024 x 1 and 1024 x 2: 172.8 vs 196.3 us at [16384, 4096],
+  // 44.2 vs 53.5 at [4096, 4096], 58.2 vs 63.4 at [4096, 5120], 177.2 vs
+  // 184.6 at [8192, 8192]; 256 x 2 lost to 512 x 1 at 2048 columns).
   bool done;
   if constexpr (MODE == 0 && C::VEC == 8) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<320, 1>,
@@ -431,15 +435,18 @@ int32_t launch_rmsnorm(const void* x, const void* res, const void* w, void* y, u
                                     RowShape<1024, 4>>(nvec, run);
   } else if constexpr (MODE == 0) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<128, 1>, RowShape<256, 1>, RowShape<512, 1>,
-                                    RowShape<1024, 1>, RowShape<1024, 2>, RowShape<1024, 3>,
+                                    RowShape<512, 2>, RowShape<512, 4>, RowShape<1024, 3>,
                                     RowShape<1024, 4>>(nvec, run);
   } else if constexpr (C::VEC == 8) {
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<256, 1>, RowShape<192, 2>,
                                     RowShape<256, 2>, RowShape<256, 3>, RowShape<512, 2>, RowShape<512, 3>,
                                     RowShape<512, 4>, RowShape<1024, 4>>(nvec, run);
   } else {
+    // fp32 FP8 rows of 1025-2048 vectors: 512 x 4 against 1024 x 2, per-token
+    // 53.7 vs 62.1 us at [4096, 5120], 117.6 vs 127.4 at [8192, 6144] (159.2
+    // vs 157.4 at [8192, 8192]); static 147.4 vs 157.5 at [8192, 8192].
     done = vec_ok && pick_row_shape<RowShape<64, 1>, RowShape<64, 2>, RowShape<128, 2>, RowShape<256, 2>,
-                                    RowShape<512, 2>, RowShape<1024, 2>, RowShape<1024, 3>,
+                                    RowShape<512, 2>, RowShape<512, 4>, RowShape<1024, 3>,
                                     RowShape<1024, 4>>(nvec, run);
   }
   if (!done) {
