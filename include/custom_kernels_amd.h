@@ -79,9 +79,10 @@ int32_t launch_fp8_quant_block_fwd(const void* x, uint8_t* x_fp8, float* scale, 
  * and the final scale overwrite; the call keeps no other state, so calls on
  * different streams may overlap. Inputs of 2^20 or more 16-byte vectors that
  * fit in the registers of a grid the GPU holds at once (up to 64 MiB of x on
- * MI355X) are read from HBM once. Where such a grid is not resident at once
- * (other work holding CUs), its waiting workgroups give up after about 2 ms
- * and each reads all of x itself: slower (one more read of x per such
+ * MI355X) are read from HBM once; larger aligned inputs are read once plus
+ * the part the registers do not hold. Where such a grid is not resident at
+ * once (other work holding CUs), its waiting workgroups give up after about
+ * 2 ms and each reads all of x itself: slower (one more read of x per such
  * workgroup, at most 511), never wrong. Replaces reference
  * csrc/includes/fp8_quant.h:51-60. */
 int32_t launch_fp8_quant_tensor_fwd(const void* x, uint8_t* x_fp8, float* scale,

@@ -206,13 +206,16 @@ def _tensor_abi(x_dev: torch.Tensor, q: torch.Tensor, scratch: torch.Tensor | No
 
 # (shape, what it reaches for bf16 / fp16; fp32 alike unless noted). The
 # one-pass form takes inputs of at most 2048 vectors (one workgroup) and of at
-# least 2^20 vectors up to what a resident grid holds in registers.
+# least 2^20 vectors; beyond what a resident grid holds in registers it
+# streams the rest of each workgroup's chunk.
 TENSOR_PATHS = [
     ((1024, 4096), "bf16/fp16: slot arrays in every cast chunk, XCD-aligned cast order; fp32: the finishing launch"),
     ((300, 4096), "slot arrays written by 75 partial workgroups (not a multiple of 8), chunks walked last-first"),
     ((2048, 4096), "one pass (config 1): 2 vectors per thread over 512 workgroups (fp32: 4)"),
     ((4096, 4096), "one pass: 4 vectors per thread over 512 workgroups (fp32: 16 over 256)"),
-    ((8192, 4096), "one pass: 16 vectors per thread over 256 workgroups, the register capacity (fp32: two passes)"),
+    ((8192, 4096), "one pass: 16 vectors per thread over 256 workgroups, the register capacity (fp32: beyond it)"),
+    ((4097, 8200), "beyond the register capacity: each resident workgroup holds 16 vectors per thread of its chunk "
+                   "and streams the rest twice; the last chunk partial"),
     ((4099, 4097), "two passes: the finishing launch, a scalar tail after the vectors"),
     ((4, 20482), "last cast chunk too short for a slot array: the finishing launch"),
     ((5, 2056), "one pass in one workgroup, no exchange (fp32: two passes, slot arrays)"),

@@ -111,7 +111,8 @@ def test_fp8_tensor_and_static_past_2g():
     """One dynamic scale over 2^31 + 49152 elements with the maximum planted
     past element 2^31: the Python API (no amax word), the reference ABI (the
     caller's int32 left holding the amax bits), the no-allocation entry point
-    (two-pass above its one-pass capacity), and a static scale."""
+    (the one-pass form streaming what its registers do not hold), and a
+    static scale."""
     from tests import _cck
 
     rows, cols = 524_300, 4096

@@ -131,7 +131,8 @@ def test_back_to_back_without_synchronising():
 @pytest.mark.parametrize("shape", [(4096, 8192), (4097, 8192)], ids=lambda s: f"{s[0]}x{s[1]}")
 def test_register_capacity_boundary(shape):
     """[4096, 8192] bf16 is 16 vectors per thread over 256 workgroups of 1024
-    threads (one pass when the GPU holds 256 at once); one more row is two passes."""
+    threads (one pass when the GPU holds 256 at once); one more row streams
+    what does not fit in registers."""
     x = inputs.randn(shape, torch.bfloat16, seed=shape[0])
     x.view(-1)[-5] = 900.0
     _check_pair(x, "e4m3")
@@ -184,6 +185,7 @@ def test_wait_fallback_reads_x_itself(dtype):
         assert lib.cck_fp8_tensor_noalloc_poll_limit(-1) == 0
         _check_pair(inputs.randn((2048, 4096), dtype, seed=71) * 3, "e4m3")
         _check_pair(inputs.randn((24, 4096), dtype, seed=72), "e5m2")
+        _check_pair(inputs.randn((4097, 8192), dtype, seed=74), "e4m3")  # beyond the register capacity
     finally:
         assert lib.cck_fp8_tensor_noalloc_poll_limit(prev) == 0
     assert lib.cck_fp8_tensor_noalloc_poll_limit(-1) == prev
