@@ -325,6 +325,7 @@ REGISTRY: dict[str, OpSpec] = {
             memory_profile="latency-bound (1.3 MB at 2048 x 160).",
             design=("E <= 8: one lane per token, every step serial in its registers",
                     "9..32 experts (up to 64 from 4096 tokens): four lanes per token over 16-expert stripes",
+                    "65..256 experts from 8192 / 12288 tokens: eight lanes per token",
                     "otherwise one wave per token, 4 experts per lane; wave arg-max per selection"),
             target="weights bit-exact against torch-CPU; indices equal the oracle's (exact ties aside)",
             reference=("baselines/moe_router.py:117-128", "csrc/kernels/moe_router.cu",

@@ -23,6 +23,7 @@
 //   * E <= 8: one lane per token (moe_router_lanes);
 //   * 9 <= E <= 32, and E <= 64 from T = 4096 on: four lanes per token, each
 //     holding its quarter of every 16-expert stripe (moe_router_groups);
+//     65 <= E <= 256 from T = 8192 (E <= 128) or 12288 on: eight lanes;
 //   * otherwise one wave per token (moe_router_waves), below.
 // One wave64 per token holds up to 256 experts (4 per lane, expert
 // e = lane + 64 * slot). The max is a wave all-reduction (DPP). The
@@ -277,7 +278,7 @@ __global__ __launch_bounds__(kLaneThreads) void moe_router_lanes(const void* __r
   for (int i = 0; i < k; ++i) topk_w[t * k + i] = renormalize ? sel[i][tid] / wsum : sel[i][tid];
 }
 
-// G lanes per token (G = 2 or 4), for n <= 16 * NS experts. The row is
+// G lanes per token (G = 2, 4 or 8), for n <= 16 * NS experts. The row is
 // cut into stripes of 16 experts (the AVX-512 vector), and lane r of a group
 // holds the CW = 16 / G experts [16 s + r CW, 16 s + (r + 1) CW) of every
 // stripe s, so each of the 16 lane classes of the softmax sum lives in one
@@ -287,23 +288,44 @@ __global__ __launch_bounds__(kLaneThreads) void moe_router_lanes(const void* __r
 // for its own classes; floating-point addition is commutative, so after the
 // cross-lane steps the lanes of a group hold the same values and all end
 // with class 0's total. Below 16 experts (one stripe) the sum is a running
-// sum handed from lane to lane instead. The max and each top-k round's arg-max are group
-// all-reductions (xor 1 and xor 2 quad permutations). Lane r of a group
-// writes the outputs of the rounds i = r mod G.
+// sum handed from lane to lane instead (G = 2 or 4). The max and each top-k
+// round's arg-max are group all-reductions (xor 1 and xor 2 quad
+// permutations, then for G = 8 the half-row mirror, which pairs each lane
+// with one of the other quad). Lane r of a group writes the outputs of the
+// rounds i = r mod G.
 constexpr int kDppRowShr1 = 0x111;     // lane i reads lane i - 1 of its row
 constexpr int kDppQuadBcast3 = 0xFF;  // quad_perm:[3,3,3,3]
 constexpr int kDppQuadBcast1 = 0xF5;  // quad_perm:[1,1,3,3]
+constexpr int kDppRowShr4 = 0x114;  // lane i reads lane i - 4 of its row
 
 template <int G, class Op>
 __device__ inline uint32_t group_allreduce(uint32_t v, Op op) {
-  static_assert(G == 2 || G == 4, "group size");
+  static_assert(G == 2 || G == 4 || G == 8, "group size");
   v = op(v, dpp<kDppQuadXor1>(v));
-  if constexpr (G == 4) v = op(v, dpp<kDppQuadXor2>(v));
+  if constexpr (G >= 4) v = op(v, dpp<kDppQuadXor2>(v));
+  // For an idempotent op, lane i combined with lane 7 - i (the other quad of
+  // its 8) completes the group.
+  if constexpr (G == 8) v = op(v, dpp<kDppRowHalfMirror>(v));
   return v;
 }
 
-// VB: bytes per row load, 16 (whole 16-byte vectors of a chunk), 8 (a
-// chunk of four 2-byte experts) or 0 (one element at a time).
+// The value of lane r ^ D of this lane's group (D = 1, 2 or 4; groups of 8
+// lanes are aligned within the 16-lane DPP rows).
+template <int D>
+__device__ inline uint32_t lane_xor(uint32_t v, int r) {
+  if constexpr (D == 1) {
+    return dpp<kDppQuadXor1>(v);
+  } else if constexpr (D == 2) {
+    return dpp<kDppQuadXor2>(v);
+  } else {
+    static_assert(D == 4, "lane distance");
+    const uint32_t up = dpp<kDppRowShl4>(v), down = dpp<kDppRowShr4>(v);
+    return (r & 4) ? down : up;
+  }
+}
+
+// VB: bytes per row load, 16 (whole 16-byte vectors of a chunk), 8 or 4 (a
+// chunk of CW experts in one 8- or 4-byte load) or 0 (one element at a time).
 template <class C, int G, int NS, int VB>
 __global__ __launch_bounds__(kLaneThreads) void moe_router_groups(const void* __restrict__ logits,
                                                                   float* __restrict__ topk_w,
@@ -312,7 +334,8 @@ __global__ __launch_bounds__(kLaneThreads) void moe_router_groups(const void* __
   constexpr int CW = kSoftmaxLanes / G;  // experts of one stripe per lane
   constexpr int PER = NS * CW;           // experts per lane
   constexpr int TPB = kLaneThreads / G;  // tokens per workgroup
-  static_assert(PER <= 32 && (VB != 16 || CW % C::VEC == 0) && (VB != 8 || CW * C::kBytes == 8),
+  static_assert(PER <= 32 && (VB != 16 || CW % C::VEC == 0) && (VB != 8 || CW * C::kBytes == 8) &&
+                    (VB != 4 || CW * C::kBytes == 4) && (G != 8 || NS >= 2),
                 "group router shape");
   __shared__ float sel[NS * kSoftmaxLanes][TPB];
   const int tid = threadIdx.x, r = tid % G, slot = tid / G;
@@ -323,13 +346,18 @@ __global__ __launch_bounds__(kLaneThreads) void moe_router_groups(const void* __
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const int e0 = kSoftmaxLanes * s + r * CW;
-    if constexpr (VB == 8) {
-      // n is a multiple of 4 and the rows are 8-byte aligned.
+    if constexpr (VB == 8 || VB == 4) {
+      // n is a multiple of CW and the rows are VB-byte aligned.
       float f[C::VEC];
       if (e0 < n) {
-        const u32x2 w = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x2*>(static_cast<const char*>(logits) + (t * n + e0) * C::kBytes));
-        C::unpack((u32x4){w.x, w.y, 0u, 0u}, f);
+        const char* a = static_cast<const char*>(logits) + (t * n + e0) * C::kBytes;
+        if constexpr (VB == 8) {
+          const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(a));
+          C::unpack((u32x4){w.x, w.y, 0u, 0u}, f);
+        } else {
+          const uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(a));
+          C::unpack((u32x4){w, 0u, 0u, 0u}, f);
+        }
       } else {
 #pragma unroll
         for (int j = 0; j < CW; ++j) f[j] = -__builtin_inff();
@@ -407,8 +435,8 @@ __global__ __launch_bounds__(kLaneThreads) void moe_router_groups(const void* __
     for (int step = kSoftmaxLanes / 2; step >= CW; step >>= 1) {
 #pragma unroll
       for (int j = 0; j < CW; ++j) {
-        const uint32_t o =
-            step / CW == 1 ? dpp<kDppQuadXor1>(f32_bits(acc[j])) : dpp<kDppQuadXor2>(f32_bits(acc[j]));
+        const uint32_t a = f32_bits(acc[j]);
+        const uint32_t o = step / CW == 1 ? lane_xor<1>(a, r) : step / CW == 2 ? lane_xor<2>(a, r) : lane_xor<4>(a, r);
         acc[j] = acc[j] + bits_f32(o);
       }
     }
@@ -492,6 +520,11 @@ void launch_router_groups(const void* logits, float* w, int64_t* idx, int64_t t,
       moe_router_groups<C, G, NS, 8><<<grid, kLaneThreads, 0, st>>>(logits, w, idx, t, n, k, renorm);
       return;
     }
+  } else if constexpr (CW * C::kBytes == 4) {
+    if (n % CW == 0 && (a & 3u) == 0) {
+      moe_router_groups<C, G, NS, 4><<<grid, kLaneThreads, 0, st>>>(logits, w, idx, t, n, k, renorm);
+      return;
+    }
   }
   moe_router_groups<C, G, NS, 0><<<grid, kLaneThreads, 0, st>>>(logits, w, idx, t, n, k, renorm);
 }
@@ -500,6 +533,15 @@ void launch_router_groups(const void* logits, float* w, int64_t* idx, int64_t t,
 // where the wave kernel's one wave per token no longer fits the GPU at once.
 constexpr int kGroupMaxExperts = 64;
 constexpr int64_t kGroupWideMinTokens = 4096;
+// Eight lanes per token (32 experts each at most) for 65 to 256 experts, from
+// enough tokens that the wave kernel's one wave per token takes several
+// rounds of the GPU: same-run A/B against it, fp32 / bf16, top-8 of 96 at
+// 8192 tokens 7.4 / 9.2 vs 13.5 / 13.6 us, top-6 of 160 at 12288 8.6 / 11.8
+// vs 14.6 / 15.7, at 16384 9.1 / 12.1 vs 18.3 / 19.6; top-8 of 256 at 16384
+// 14.7 / 18.5 vs 24.0 / 26.1. Below those counts the wave kernel's shorter
+// chain wins (top-6 of 160 at 2048 tokens: 5.4 vs 6.8 us fp32).
+constexpr int kGroup8MaxExperts = 256;
+inline int64_t group8_min_tokens(int n) { return n <= 128 ? 8192 : 12288; }
 
 }  // namespace
 
@@ -518,6 +560,16 @@ extern "C" int32_t launch_moe_router_fwd(const void* logits, float* topk_weights
     using C = decltype(codec);
     if (small_grid && n <= kLaneMaxExperts) {
       launch_router_lanes<C, kLaneMaxExperts>(logits, topk_weights, topk_indices, num_tokens, n, kk, rn, st);
+      return launch_status();
+    }
+    if (small_grid && n > kGroupMaxExperts && n <= kGroup8MaxExperts && num_tokens >= group8_min_tokens(n)) {
+      if (n <= 8 * kSoftmaxLanes) {
+        launch_router_groups<C, 8, 8>(logits, topk_weights, topk_indices, num_tokens, n, kk, rn, st);
+      } else if (n <= 10 * kSoftmaxLanes) {
+        launch_router_groups<C, 8, 10>(logits, topk_weights, topk_indices, num_tokens, n, kk, rn, st);
+      } else {
+        launch_router_groups<C, 8, 16>(logits, topk_weights, topk_indices, num_tokens, n, kk, rn, st);
+      }
       return launch_status();
     }
     if (small_grid && groups) {

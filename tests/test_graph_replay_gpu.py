@@ -163,8 +163,9 @@ def test_moe_ops_graph():
     eo2, ui2, w2 = [t.cuda() for t in sets_c2[0]]
     out2 = torch.empty(64, 4104, dtype=BF16, device="cuda")
     _replay_matches_eager([eo2, ui2, w2], [out2], lambda: native.token_combine_fwd(eo2, ui2, w2, out2), sets_c2)
-    # the router's three forms: a wave per token (160 experts), four lanes (32), one lane (8)
-    for t, e, k in ((512, 160, 6), (512, 32, 8), (4096, 8, 2)):
+    # the router's forms: a wave per token (160 experts), eight lanes (160 at 12288 tokens), four lanes (32),
+    # one lane (8)
+    for t, e, k in ((512, 160, 6), (12288, 160, 6), (512, 32, 8), (4096, 8, 2)):
         sets_r = [[inputs.router_inputs(t, e, torch.bfloat16, seed=s)] for s in range(3)]
         lg = sets_r[0][0].cuda()
         tw, ti = torch.empty(t, k, device="cuda"), torch.empty(t, k, dtype=torch.int64, device="cuda")

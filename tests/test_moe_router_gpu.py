@@ -14,9 +14,11 @@ way; the kernel takes the lower expert index).
 
 Up to 8 experts one lane holds a token; a group of four lanes (16-expert
 stripes) holds one of 9 to 32 experts, and of up to 64 from 4096 tokens on;
-otherwise a wave does: the cases cover each form's edges (expert counts
-around 8, 16, 32 and 64, k = E, token counts that leave a partial workgroup
-or cross 4096) and rows that are not 16-byte aligned.
+a group of eight lanes one of 65 to 256 experts from 8192 tokens (up to 128
+experts) or 12288; otherwise a wave does: the cases cover each form's edges
+(expert counts around 8, 16, 32, 64, 128 and 256, k = E, token counts that
+leave a partial workgroup or cross the thresholds) and rows that are not
+16-byte aligned.
 """
 
 from __future__ import annotations
@@ -37,7 +39,9 @@ CASES = [(2048, 8, 2, True), (2048, 160, 6, True), (1024, 32, 1, True), (1024, 3
          (3, 33, 33, False), (77, 48, 7, True), (50, 64, 64, True), (129, 65, 9, True), (31, 127, 5, True),
          (97, 128, 16, True), (40, 129, 8, True), (4100, 8, 2, True), (1000, 32, 8, False), (4095, 48, 6, True),
          (4096, 48, 6, True), (4101, 64, 64, False), (4097, 33, 5, True), (33, 5, 5, True), (70, 3, 2, False),
-         (200, 13, 4, False), (64, 15, 15, True), (129, 10, 1, True)]
+         (200, 13, 4, False), (64, 15, 15, True), (129, 10, 1, True),
+         (8192, 65, 5, True), (8193, 100, 8, False), (8191, 128, 8, True), (12288, 160, 6, True),
+         (12289, 256, 8, True), (12290, 129, 129, False)]
 
 
 def _check(logits, k, renorm):
@@ -93,17 +97,34 @@ def test_router_unaligned_rows(e, dtype):
     assert torch.equal(torch.gather(p, 1, i.cpu()), torch.gather(p, 1, torch.topk(p, k).indices))
 
 
-@pytest.mark.parametrize("e", [12, 32, 100])
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("e", [72, 160, 256])
+def test_router_eight_lane_groups_unaligned(e, dtype):
+    """The eight-lane form on rows one element past a 16-byte boundary (element loads)."""
+    t, k = 12300, 6
+    logits = inputs.router_inputs(t, e, dtype, seed=e + 1)
+    flat = torch.empty(t * e + 1, dtype=dtype, device="cuda")
+    dev = flat[1:].view(t, e)
+    dev.copy_(logits.cuda())
+    w, i = moe_router(dev, k)
+    w_ref, _ = moe.moe_router_avx512(logits, k)
+    assert torch.equal(w.cpu().view(torch.int32), w_ref.view(torch.int32))
+    p = moe.softmax_probs(logits)
+    assert torch.equal(torch.gather(p, 1, i.cpu()), torch.gather(p, 1, torch.topk(p, k).indices))
+
+
+@pytest.mark.parametrize("e", [12, 32, 100, 200])
 def test_router_ties_across_lanes_and_minus_inf(e):
     """Equal maxima held by different lanes of a token's group, and -inf
     logits (probability +0, picked last, lowest index first)."""
-    logits = torch.full((9, e), -float("inf"))
+    t = 9 if e <= 64 else 12289  # past the eight-lane threshold
+    logits = torch.full((t, e), -float("inf"))
     picks = [1, e // 2 - 1, e // 2 + 3, e - 2]
     logits[:, picks] = 1.5
     logits[:, 0] = 0.25
     w, i = moe_router(logits.cuda(), 6)
     i = i.cpu()
-    assert torch.equal(i[:, :5], torch.tensor([picks + [0]] * 9))
+    assert torch.equal(i[:, :5], torch.tensor([picks + [0]] * t))
     assert bool((i[:, 5] == 2).all())  # the lowest index among the +0 probabilities
     w_ref, _ = moe.moe_router_avx512(logits, 6)
     assert torch.equal(w.cpu().view(torch.int32), w_ref.view(torch.int32))
