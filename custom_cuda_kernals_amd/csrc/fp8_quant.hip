@@ -806,7 +806,6 @@ int onepass_groups() {
 // 16.67; [8192, 4096] 24.04 / 22.12 against 29.66 / 27.76.
 constexpr int64_t kOnePassMinVecs = int64_t(1) << 20;
 constexpr int64_t kOnePassSoloVecs = (int64_t)kOnePassThreads * 2;  // one workgroup: no exchange
-constexpr bool kOnePassSpill = true;
 
 // Launches the one-pass form where it pays: inputs one workgroup holds
 // (no exchange and no init launch: the fewest vectors per thread that
@@ -838,7 +837,7 @@ bool launch_onepass(const void* x, uint8_t* q, float* scale, int32_t* amax_scrat
       attempt(IntC<16>{}, IntC<4>{})) {
     return true;
   }
-  if (nvec <= kOnePassSoloVecs || !kOnePassSpill) return false;
+  if (nvec <= kOnePassSoloVecs) return false;
   // Beyond what the grid holds: every resident workgroup takes an equal
   // chunk, 16 vectors per thread of it in registers and the rest streamed.
   constexpr int U = 16, WPE = 4;
