@@ -170,8 +170,9 @@ constexpr int kPolQ = kPolSC1 | kPolNT;
 // selects the LDS SiLU table, filled while the first row's loads are in
 // flight. STATIC uses static_scale and skips the row reduction; each thread's
 // own max |y| then selects the fast or exact conversion for its vectors.
-// LDSY (rows of more than four vectors per thread): y is parked in LDS, in
-// slots only its own thread reads back, instead of registers; 1024 x 8
+// LDSY (rows of more than four vectors per thread, and most bf16 per-token
+// rows of three or four): y is parked in LDS, in slots only its own thread
+// reads back, instead of registers; 1024 x 8
 // vectors hold rows of 65536 bf16 / fp16 (32768 fp32) elements in 128 KB.
 // The raw registers are then free after the SiLU, so the next row's loads go
 // out before the amax reduction.
@@ -325,20 +326,46 @@ bool launch_swiglu_fp8_rows(const void* gate, const void* up, uint8_t* yq, float
     // The table pays for its per-workgroup fill only on long rows. Static
     // scales use these rows only from 768 threads (the flat stream otherwise).
     constexpr bool kTab = std::is_same_v<C, CodecBF16> && S::kThreads * S::kItems >= 1152;
-    constexpr bool kLdsY = S::kItems > 4;
-    if constexpr (!STATIC || (kTab && S::kThreads >= 768 && !kLdsY)) {
+    auto go = [&](auto ldsy) {
+      constexpr bool kLdsY = decltype(ldsy)::value;
       constexpr auto kernel = swiglu_fp8_resident<C, S::kThreads, S::kItems, FMT, kTab, STATIC, kLdsY>;
-      // bf16 rows with y in LDS (one 128 KB workgroup per CU) run on a grid
-      // of the workgroups the device holds at once, each looping over rows:
-      // one SiLU table fill per workgroup instead of per row, and no idle CU
-      // between rows (4096 rows: 194.5 against 209.8 us at 53248 columns,
-      // 239.8 against 263.6 at 65536). The same grid loses on every other
-      // row shape (config 3v 100.5 against 89.8 us; fp16 LDS rows 5-18 %).
+      // bf16 rows with y in LDS run on a grid of the workgroups the device
+      // holds at once, each looping over rows: one SiLU table fill per
+      // workgroup instead of per row, no idle CU between rows, and the next
+      // row's loads in flight across the amax reduction (4096 rows: 194.5
+      // against 209.8 us at 53248 columns, 239.8 against 263.6 at 65536).
+      // The same grid loses on register-resident rows (config 3v 100.5
+      // against 89.8 us) and on fp16 LDS rows (5-18 %).
       constexpr bool kLoop = kTab && kLdsY;
       const int64_t resident = kLoop ? resident_groups<kernel>(S::kThreads) : 0;
       const unsigned grid = resident > 0 && resident < (int64_t)g ? (unsigned)resident : g;
       kernel<<<grid, S::kThreads, 0, st>>>(gate, up, yq, scale, static_scale, rows, cols);
       launched = true;
+    };
+    if constexpr (S::kItems > 4) {
+      if constexpr (!STATIC) go(std::true_type{});
+    } else if constexpr (kTab && !STATIC && S::kThreads == 1024 && S::kItems >= 3) {
+      // bf16 per-token rows of three and four vectors per thread park y in
+      // LDS (48 / 64 KB) on the looping grid too, where the grid loops (more
+      // rows than resident workgroups) and at most 3/4 of the threads hold
+      // a last vector. Same-run A/B against y in registers with one
+      // workgroup per row, 8192 rows: 16896 columns 119.1 against 125.7 us,
+      // 18944 127.3 / 140.7, 22016 146.4 / 156.4, 25600 180.6 / 186.6,
+      // 28672 190.6 / 202.1, 30720 204.5 / 216.2; 1024 rows of 28672 29.0 /
+      // 31.4. Past that fill it lost: 23040 168.6 / 163.9, 23552 172.2 /
+      // 168.5, 31744 236.0 / 231.3, 32768 238.0 / 230.5 (24576 tied); so
+      // did a grid that does not loop (256 rows of 28672: 9.5 / 9.0) and
+      // fp16 and fp32 rows (1-4 %).
+      constexpr auto kParked = swiglu_fp8_resident<C, S::kThreads, S::kItems, FMT, kTab, STATIC, true>;
+      const int64_t last = nvec - (int64_t)(S::kItems - 1) * S::kThreads;  // threads holding a last vector
+      const int64_t resident = resident_groups<kParked>(S::kThreads);
+      if (4 * last <= 3 * S::kThreads && resident > 0 && resident < rows) {
+        go(std::true_type{});
+      } else {
+        go(std::false_type{});
+      }
+    } else if constexpr (!STATIC || (kTab && S::kThreads >= 768)) {
+      go(std::false_type{});
     }
   };
   // bf16 rows from a sweep over THREADS 256..1024 (step 128) x ITEMS 1..4,

@@ -89,7 +89,7 @@ def test_swiglu_fp8_small(shape, dtype, fmt, static):
 # Row lengths that reach every register-resident shape of both kernels (the
 # largest row each shape holds, and one vector past some of them).
 BUCKET_COLS = [64, 512, 1024, 2048, 2056, 2560, 3072, 3584, 4096, 5120, 6144, 6152, 7176, 8192, 9216, 10240, 12288,
-               16384, 20480, 24576, 32768, 40960, 53248, 65536]
+               16384, 20480, 24576, 28672, 32768, 40960, 53248, 65536]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
@@ -99,6 +99,17 @@ def test_every_row_shape_bucket(cols, dtype):
     _check_rms(x, r, w, 1e-5, "e4m3", None)
     _check_rms(x, r, w, 1e-5, "e4m3", 0.05)
     g, u = inputs.swiglu_inputs(3, cols, dtype, seed=cols + 1)
+    _check_swiglu(g, u, "e4m3", None)
+
+
+@pytest.mark.parametrize("shape", [(513, 20480), (512, 20480), (600, 22528), (600, 22536), (257, 30720),
+                                   (257, 30728), (256, 28672)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_swiglu_fp8_parked_row_edges(shape):
+    """bf16 per-token rows of 1024 x 3 and 1024 x 4 vectors park y in LDS
+    on a looping grid only when there are more rows than resident
+    workgroups and at most 3/4 of the threads hold a last vector: row counts
+    and lengths on both sides of those two edges."""
+    g, u = inputs.swiglu_inputs(*shape, torch.bfloat16, seed=shape[1] + shape[0])
     _check_swiglu(g, u, "e4m3", None)
 
 

@@ -2,7 +2,8 @@
 take a second row after the grid cap, at row lengths that select every
 register-resident shape of the RMSNorm (+ FP8), per-token FP8 and
 SwiGLU + FP8 launchers (one to four vectors per thread, the weight held
-across rows, y held packed, y parked in LDS for rows of 53248), against the
+across rows, y held packed, y parked in LDS for bf16 per-token rows of
+20480, 28672 and 53248), against the
 CPU oracle on the first rows, rows in the middle and the rows each looping
 workgroup took second.
 """
@@ -96,7 +97,7 @@ def test_swiglu_fp8_lds_rows_loop(dtype, cols):
         assert_f32_bits_equal(s[sl], s_ref.reshape(s[sl].shape), f"scales rows {sl}")
 
 
-@pytest.mark.parametrize("cols", [8192, 12288, 20480, 53248])
+@pytest.mark.parametrize("cols", [8192, 12288, 20480, 24576, 28672, 53248])
 @pytest.mark.parametrize("static", [None, 0.05], ids=["token", "static"])
 def test_swiglu_fp8_rows_loop(cols, static):
     gate, up = _randn((ROWS, cols), cols + 4), _randn((ROWS, cols), cols + 5)
