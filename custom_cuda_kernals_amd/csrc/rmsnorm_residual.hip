@@ -402,7 +402,10 @@ int32_t launch_rmsnorm(const void* x, const void* res, const void* w, void* y, u
     // workgroup): per-token from 1536 vectors of capacity (8192 bf16 rows:
     // 126.9 against 134.6 us at 12288 columns, 286.1 against 301.5 at 24576;
     // fp16 172.8 against 184.9 at 16384), static from 3072 (273.3 against
-    // 297.7 at 24576). Plain RMSNorm rows lose 3-6 % on such a grid.
+    // 297.7 at 24576). Plain RMSNorm rows lose 3-6 % on such a grid, and so
+    // do narrower per-token rows even with the next-row prefetch: from 1024
+    // vectors, 81.0 against 76.1 us at [8192, 8192]; from 512, 84.0 against
+    // 74.9 at [16384, 4096].
     constexpr int kCap = S::kThreads * S::kItems;
     constexpr bool kLoop = (MODE == 1 && kCap >= 1536) || (MODE == 2 && kCap >= 3072);
     auto go = [&](auto full) {
