@@ -121,6 +121,36 @@ __global__ __launch_bounds__(THREADS) void token_gather_rows_pf(const u32x4* __r
   }
 }
 
+// Large gathers: one 16-byte vector per thread, waves of 64 consecutive
+// destination vectors, on a grid of up to 2^20 workgroups, the shape of a flat
+// copy. A wave's rows and source indices are wave-uniform (scalar loads); rows
+// of at least 64 vectors put a wave in at most two rows.
+__global__ __launch_bounds__(256) void token_gather_flat(const u32x4* __restrict__ src,
+                                                         const int64_t* __restrict__ idx,
+                                                         u32x4* __restrict__ dst, int64_t n_dst,
+                                                         int64_t row_vecs, int64_t n_src) {
+  const int64_t total = n_dst * row_vecs;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  for (int64_t base = (int64_t)blockIdx.x * 256 + wave * 64; base < total; base += (int64_t)gridDim.x * 256) {
+    const int64_t row = base / row_vecs;
+    const int64_t col0 = base - row * row_vecs;
+    int64_t s = idx[row];
+    int64_t col = col0 + lane;
+    if (col0 + 64 > row_vecs) {  // the wave ends in the next row
+      const int64_t s1 = row + 1 < n_dst ? idx[row + 1] : -1;
+      if (col >= row_vecs) {
+        s = s1;
+        col -= row_vecs;
+      }
+    }
+    const bool in = base + lane < total;
+    u32x4 v = (u32x4){0u, 0u, 0u, 0u};
+    if (in && s >= 0 && s < n_src) v = ld_stream(src + s * row_vecs + col);
+    if (in) st_stream(v, dst + base + lane);
+  }
+}
+
 // Any row length / alignment: element-wise (E = 1-, 2- or 4-byte element).
 template <class E>
 __global__ __launch_bounds__(256) void token_gather_elems(const E* __restrict__ src,
@@ -381,6 +411,15 @@ inline int32_t elem_bytes(int32_t dtype) {
 // 16384 rows, 191.3 vs 194.7 at 65536 (with the index prefetch below);
 // 1024 -> 2048 rows took 7.5 vs 6.9 us with 8 (a grid of 256 workgroups).
 constexpr int64_t kGatherR8Min = 4096;
+// From 2^22 destination vectors (64 MiB) on, rows of at least 64 vectors take
+// token_gather_flat. Same-run A/B on MI355X, bf16 (fp32) rows, against the
+// row kernels below: 65536 -> 65536 rows of 4096 171.9 vs 190.8 us, 16384
+// rows 43.6 vs 46.8, 8192 rows 23.0 vs 24.0, 32768 rows of 2048 44.1 vs
+// 47.1, 65536 rows of 1024 44.4 vs 47.3, 16384 -> 32768 rows of 7168 149.3
+// vs 152.3; fp32 16384 rows of 4096 85.6 vs 89.1, 65536 rows 348.3 vs 358.7.
+// Below it the row kernels win: 4096 rows of 4096, 11.8 vs 12.6 us;
+// 8192 -> 16384 rows of 1024, 11.8 vs 12.6.
+constexpr int64_t kGatherFlatMin = int64_t(1) << 22;
 
 int32_t gather(const void* src, const int64_t* indices, void* dst, int64_t n_dst, int64_t h,
                int32_t dtype, int64_t n_src, hipStream_t st) {
@@ -391,7 +430,10 @@ int32_t gather(const void* src, const int64_t* indices, void* dst, int64_t n_dst
   const int64_t row_bytes = h * es;
   if (row_bytes % 16 == 0 && host_aligned(src, 16) && host_aligned(dst, 16)) {
     const int64_t rv = row_bytes / 16;
-    if (rv <= 512) {
+    if (rv >= 64 && n_dst * rv >= kGatherFlatMin) {
+      token_gather_flat<<<flat_grid(n_dst * rv, 256, 1 << 20), 256, 0, st>>>(
+          static_cast<const u32x4*>(src), indices, static_cast<u32x4*>(dst), n_dst, rv, n_src);
+    } else if (rv <= 512) {
       // One vector per thread, up to 512 threads, R rows per workgroup step:
       // with R = 4, 12.3 vs 12.6 us for one row per workgroup at 2048 -> 4096
       // rows of 8 KB on MI355X (13.0-13.5 with 2-8 vectors per thread).

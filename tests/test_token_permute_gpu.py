@@ -64,12 +64,15 @@ def test_gather_vector_tails(dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("n_src, n_dst, h", [(3000, 4095, 512), (3000, 4097, 512), (5000, 100003, 64),
-                                             (700, 70001, 8), (300, 1031, 8200), (300, 517, 4100)])
+                                             (700, 70001, 8), (300, 1031, 8200), (300, 517, 4100),
+                                             (3000, 4099, 8200), (5000, 65537, 512)])
 def test_gather_row_forms(n_src, n_dst, h, dtype):
     """The gather's launch forms: 4 and 8 rows per workgroup step around 4096
     destination rows, the resident grid with prefetched indices (many short
-    rows), and rows of more than 1024 vectors (4 in flight per thread); a few
-    indices out of range in each."""
+    rows), rows of more than 1024 vectors (4 in flight per thread), and the
+    flat form from 2^22 destination vectors (waves that span two rows, a
+    partial last wave, rows of exactly 64 vectors); a few indices out of
+    range in each."""
     src, idx = inputs.gather_inputs(n_src, n_dst, h, dtype, seed=n_dst + h)
     idx[::997] = n_src  # out of range: zero rows
     out = token_gather(src.cuda(), idx.cuda()).cpu()
