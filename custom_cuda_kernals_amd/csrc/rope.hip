@@ -30,14 +30,14 @@ using RopeRow = RowBuf<TOK == 1, TOK == 1 ? (kPolSC1 | kPolNT) : kBufStorePolicy
 // q / k and q_out / k_out may be the same buffers (in place), so none of
 // the four is declared __restrict__; each element is loaded before the
 // element is stored, by the same thread.
-template <class C, int CHUNKS, int TOK>
-__global__ __launch_bounds__(256) void rope_tokens(const void* q, const void* k,
+template <class C, int CHUNKS, int TOK, int NT = 256>
+__global__ __launch_bounds__(NT) void rope_tokens(const void* q, const void* k,
                                                    const float* __restrict__ cos_t,
                                                    const float* __restrict__ sin_t, void* q_out,
                                                    void* k_out, int64_t tokens, int64_t seq_len,
                                                    int hq, int hkv, int head_dim) {
   constexpr int VEC = C::VEC;
-  constexpr int LANES = 256 / TOK;          // threads per token
+  constexpr int LANES = NT / TOK;           // threads per token
   constexpr int HLANES = LANES / CHUNKS;    // head lanes per token
   const int t_local = TOK == 1 ? 0 : threadIdx.x / LANES;
   const int c = threadIdx.x % CHUNKS;
@@ -111,6 +111,24 @@ __global__ __launch_bounds__(256) void rope_scalar(const void* q, const void* k,
   }
 }
 
+// One token per workgroup of 64 * W threads for the W in WS that equals
+// `waves`: a thread per (head, chunk) of the token, so no thread rotates a
+// second head after its first. false (nothing launched) if none matches.
+template <class C, int CHUNKS, int... WS>
+bool launch_rope_per_head(int waves, std::integer_sequence<int, WS...>, const void* q, const void* k,
+                          const float* ct, const float* sn, void* q_out, void* k_out, int64_t tokens,
+                          int64_t seq_len, int hq, int hkv, int d, hipStream_t st) {
+  const unsigned grid = flat_grid(tokens, 1, kMaxRowGroups);
+  auto one = [&](auto w) {
+    constexpr int W = decltype(w)::value;
+    if (waves != W) return false;
+    rope_tokens<C, CHUNKS, 1, 64 * W><<<grid, 64 * W, 0, st>>>(q, k, ct, sn, q_out, k_out, tokens, seq_len, hq,
+                                                               hkv, d);
+    return true;
+  };
+  return (one(std::integral_constant<int, WS>{}) || ...);
+}
+
 }  // namespace
 }  // namespace cck
 
@@ -142,7 +160,22 @@ extern "C" int32_t launch_rope_fwd(const void* q, const void* k, const void* cos
 #define CCK_ROPE(CH_, TOK_, LDS_)                                                            \
   rope_tokens<C, CH_, TOK_><<<flat_grid(tokens, TOK_, kMaxRowGroups), 256, LDS_, st>>>(    \
       q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d)
-    if (chunks == 8) {
+    // Tokens of more than 256 / CHUNKS heads (and at most 1024 / CHUNKS) get a
+    // thread per (head, chunk) in one workgroup of that many threads, rounded
+    // up to whole waves, instead of 256 threads that take the heads in
+    // rounds. Same-run A/B on MI355X, bf16 head_dim 128, graph-replayed:
+    // 32 / 8 heads (320 threads) 15.30 vs 15.72 us at [2, 2048], 52.40 vs
+    // 52.85 at [16, 1024], 103.55 vs 103.43 at config 4; 64 / 8 heads (576)
+    // 25.47 vs 26.29 at [1, 4096], 48.20 vs 49.53 at [1, 8192]; 32 / 32
+    // heads (512) 82.62 vs 84.41 at [4, 4096].
+    const int heads = hq + hkv;
+    const int waves = chunks > 0 ? (heads * chunks + 63) / 64 : 0;
+    if ((chunks == 8 || chunks == 16) && heads * chunks > 256 && waves <= 16 &&
+        (chunks == 8 ? launch_rope_per_head<C, 8>(waves, std::integer_sequence<int, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16>{},
+                                                  q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d, st)
+                     : launch_rope_per_head<C, 16>(waves, std::integer_sequence<int, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16>{},
+                                                   q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d, st))) {
+    } else if (chunks == 8) {
       // Measured fastest on MI355X for head_dim 128 bf16, with at most 6
       // workgroups per CU (8 fit): 102.0 vs 103.8 us at config 4.
       CCK_ROPE(8, 1, kLdsForGroupsPerCu<6>);

@@ -21,7 +21,11 @@ pytestmark = pytest.mark.gpu
 CASES = [(4, 128, 12, 12, 64), (2, 2048, 32, 8, 128), (1, 4096, 32, 8, 128), (3, 17, 8, 2, 64),
          (8, 1, 8, 8, 64), (1, 8192, 8, 8, 64), (0, 128, 8, 8, 64), (1, 1, 1, 1, 64), (2, 32, 4, 1, 16),
          # head_dim 256 / 512: 32 and 16 chunk lanes (one and two tokens per workgroup)
-         (2, 16, 4, 2, 256), (1, 8, 3, 1, 512)]
+         (2, 16, 4, 2, 256), (1, 8, 3, 1, 512),
+         # a thread per (head, chunk) in workgroups of 5-16 waves: 72, 64, 33 and 128 heads of 128 (8 chunk
+         # lanes; fp32 16: 1152 threads fall back to rounds), 48 and 129 heads of 64 (fp32: 8 chunk lanes)
+         (1, 64, 64, 8, 128), (2, 33, 32, 32, 128), (1, 50, 29, 4, 128), (1, 20, 120, 8, 128), (3, 7, 40, 8, 64),
+         (1, 9, 100, 29, 64)]
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
 
 
