@@ -167,7 +167,8 @@ extern "C" int32_t launch_rope_fwd(const void* q, const void* k, const void* cos
     // 32 / 8 heads (320 threads) 15.30 vs 15.72 us at [2, 2048], 52.40 vs
     // 52.85 at [16, 1024], 103.55 vs 103.43 at config 4; 64 / 8 heads (576)
     // 25.47 vs 26.29 at [1, 4096], 48.20 vs 49.53 at [1, 8192]; 32 / 32
-    // heads (512) 82.62 vs 84.41 at [4, 4096].
+    // heads (512) 82.62 vs 84.41 at [4, 4096]. Capping these at 4, 5 or 6
+    // workgroups per CU (LDS reserved) measured no different.
     const int heads = hq + hkv;
     const int waves = chunks > 0 ? (heads * chunks + 63) / 64 : 0;
     if ((chunks == 8 || chunks == 16) && heads * chunks > 256 && waves <= 16 &&
