@@ -154,6 +154,11 @@ def test_moe_ops_graph():
     src, idx = [t.cuda() for t in sets_g[0]]
     dst = torch.empty(1024, 4096, dtype=BF16, device="cuda")
     _replay_matches_eager([src, idx], [dst], lambda: native.token_gather_fwd(src, idx, dst), sets_g)
+    # 8192 rows of 4096: 2^22 destination vectors, the flat gather form
+    sets_f = [list(inputs.gather_inputs(1024, 8192, 4096, BF16, seed=s)) for s in range(3)]
+    src_f, idx_f = [t.cuda() for t in sets_f[0]]
+    dst_f = torch.empty(8192, 4096, dtype=BF16, device="cuda")
+    _replay_matches_eager([src_f, idx_f], [dst_f], lambda: native.token_gather_fwd(src_f, idx_f, dst_f), sets_f)
     sets_c = [list(inputs.combine_inputs(256, 6, 4096, BF16, seed=s)) for s in range(3)]
     eo, ui, w = [t.cuda() for t in sets_c[0]]
     out = torch.empty(256, 4096, dtype=BF16, device="cuda")

@@ -46,10 +46,12 @@ def test_gather_matches_oracle(case, dtype):
 
 
 @pytest.mark.parametrize("fmt", [torch.float8_e4m3fn, torch.float8_e5m2])
-@pytest.mark.parametrize("h", [4096, 100, 7])
-def test_gather_fp8_rows(fmt, h):
+@pytest.mark.parametrize("h, n_dst", [(4096, 777), (100, 777), (7, 777), (4096, 16400)])
+def test_gather_fp8_rows(fmt, h, n_dst):
+    """FP8 code rows move as bytes; 16400 rows of 4096 codes take the flat
+    form (2^22 destination vectors and more)."""
     src = torch.randint(0, 256, (300, h), dtype=torch.uint8).view(fmt)
-    idx = torch.randint(0, 300, (777,))
+    idx = torch.randint(0, 300, (n_dst,))
     out = token_gather(src.cuda(), idx.cuda()).cpu()
     assert torch.equal(out.view(torch.uint8), src.view(torch.uint8)[idx])
 
