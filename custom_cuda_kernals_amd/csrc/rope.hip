@@ -177,8 +177,9 @@ extern "C" int32_t launch_rope_fwd(const void* q, const void* k, const void* cos
                      : launch_rope_per_head<C, 16>(waves, std::integer_sequence<int, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16>{},
                                                    q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d, st))) {
     } else if (chunks == 8) {
-      // Measured fastest on MI355X for head_dim 128 bf16, with at most 6
-      // workgroups per CU (8 fit): 102.0 vs 103.8 us at config 4.
+      // Tokens of at most 32 heads (and more than 128): with at most 6
+      // workgroups per CU (8 fit) this 256-thread shape measured 102.0 vs
+      // 103.8 us on MI355X at config 4's size when that took it too.
       CCK_ROPE(8, 1, kLdsForGroupsPerCu<6>);
     } else if (chunks == 4) {
       // bf16 head_dim 64: 64.1 vs 67.8 us for eight tokens per workgroup;
