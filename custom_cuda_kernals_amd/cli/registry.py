@@ -245,8 +245,9 @@ REGISTRY: dict[str, OpSpec] = {
             formula="o1 = x1 c - x2 s; o2 = x2 c + x1 s, each product and difference rounded to fp32",
             dtypes=("float32", "float16", "bfloat16"),
             memory_profile="HBM-bound: 2 B in + 2 B out per bf16 element plus the tables (config 4: 673 MB).",
-            design=("one workgroup per token walking all 40 heads, so cos / sin are read once per token",
-                    "per-token buffer-resource stores with SC1 | NT; at most 6 workgroups per CU"),
+            design=("one workgroup per token, a thread per (head, chunk) for 33-128 heads (320 threads at "
+                    "config 4's 40), cos / sin read once per chunk",
+                    "per-token buffer-resource stores with SC1 | NT"),
             target=">= 75 % of 8 TB/s at q [8, 4096, 32, 128] + k [8, 4096, 8, 128] bf16; bit-exact",
             reference=("baselines/rope.py:103-145", "csrc/kernels/rope.cu", "csrc/includes/rope.h:23-36"),
             python_api=("rope",), c_entry_points=("launch_rope_fwd",), sources=(_CSRC + "rope.hip",),
@@ -290,7 +291,9 @@ REGISTRY: dict[str, OpSpec] = {
             formula="the swiglu formula, then per-row (or static) FP8 of y as stored in its dtype",
             dtypes=("float32", "float16", "bfloat16"),
             memory_profile="HBM-bound: 4 B in + 1 B out per bf16 element (config 3v: 587 MB, 5b: 1.17 GB).",
-            design=("1024 x 2 rows; the bf16 SiLU tabulated in LDS (4864 entries) and looked up per gate",),
+            design=("1024 x 2 rows; the bf16 SiLU tabulated in LDS (4864 entries) and looked up per gate",
+                    "wider bf16 per-token rows park y in LDS on a looping grid, the next row loaded across the "
+                    "amax reduction"),
             target=">= 75 % of 8 TB/s at [8192 | 16384, 14336] bf16; bit-exact vs the composed eager op",
             reference=("baselines/swiglu.py:107-112", "baselines/fp8_quant.py:162-178"),
             python_api=("swiglu_fp8",), c_entry_points=("launch_swiglu_fp8_fwd",), sources=(_CSRC + "swiglu.hip",),
@@ -303,7 +306,8 @@ REGISTRY: dict[str, OpSpec] = {
             formula="dst[i] = src[idx[i]]; out[t] = sum_j w[t, j] * eo[ui[t, j]] (fp32, j order)",
             dtypes=("float32", "float16", "bfloat16", "fp8 (gather)"),
             memory_profile="HBM-bound row moves (gather 67 MB, combine k = 2 50 MB at the reference's shapes).",
-            design=("four destination rows per gather workgroup", "two expert rows in flight per combine step",
+            design=("four or eight destination rows per gather workgroup; one vector per thread on a flat grid "
+                    "from 2^22 destination vectors", "two expert rows in flight per combine step",
                     "the permutation bookkeeping as one stable counting-sort launch (compute_permutation with "
                     "num_experts)"),
             target="gather and the permutation bit-exact; combine equal to the j-order fp32 sum",
