@@ -279,7 +279,9 @@ REGISTRY: dict[str, OpSpec] = {
             formula="the rmsnorm_residual formula, then per-row (or static) FP8 of y as stored in its dtype",
             dtypes=("float32", "float16", "bfloat16"),
             memory_profile="HBM-bound: 4 B in + 2 B + 1 B out per bf16 element (config 5a: 470 MB).",
-            design=("256 x 2 rows, y kept as fp32 in registers across the amax reduction",),
+            design=("256 x 2 rows, y kept as fp32 in registers across the amax reduction",
+                    "per-token rows of 1536+ vectors loop on a resident grid, the next row loaded across the amax "
+                    "reduction"),
             target=">= 75 % of 8 TB/s at [16384, 4096] bf16; codes and scales bit-exact vs the composed eager op",
             reference=("baselines/rmsnorm_residual.py:123-136", "baselines/fp8_quant.py:162-178"),
             python_api=("rmsnorm_residual_fp8",), c_entry_points=("launch_rmsnorm_residual_fp8_fwd",),
