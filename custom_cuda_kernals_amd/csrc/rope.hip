@@ -8,10 +8,12 @@
 //   out[:D/2] = T(x1*cos - x2*sin),  out[D/2:] = T(x2*cos + x1*sin)
 // so the output is bit-identical to the eager oracle given the same tables.
 //
-// Design: a 256-thread workgroup owns TOK tokens. Within a token, a thread is
-// pinned to one VEC-wide chunk of the half dimension and walks the heads
-// (q heads first, then k heads) with a stride of the number of head lanes,
-// so its cos/sin chunk is loaded once per token and reused for every head.
+// Design: a workgroup owns TOK tokens. Within a token, a thread is pinned to
+// one VEC-wide chunk of the half dimension and walks the heads (q heads
+// first, then k heads) with a stride of the number of head lanes, so its
+// cos/sin chunk is loaded once per token and reused for every head it takes.
+// Workgroups are 256 threads, or, for one token of more heads than 256
+// threads cover at once, a thread per (head, chunk) of the token.
 // All accesses are 16 bytes; a wave covers whole 128-byte cache lines.
 #include "launch.hpp"
 
@@ -113,17 +115,23 @@ __global__ __launch_bounds__(256) void rope_scalar(const void* q, const void* k,
 
 // One token per workgroup of 64 * W threads for the W in WS that equals
 // `waves`: a thread per (head, chunk) of the token, so no thread rotates a
-// second head after its first. false (nothing launched) if none matches.
+// second head after its first. With min_rounds > 0, not when the tokens
+// fill more than one but fewer than min_rounds rounds of the workgroups the
+// device holds at once. false (nothing launched) otherwise.
 template <class C, int CHUNKS, int... WS>
-bool launch_rope_per_head(int waves, std::integer_sequence<int, WS...>, const void* q, const void* k,
-                          const float* ct, const float* sn, void* q_out, void* k_out, int64_t tokens,
-                          int64_t seq_len, int hq, int hkv, int d, hipStream_t st) {
+bool launch_rope_per_head(int waves, int min_rounds, std::integer_sequence<int, WS...>, const void* q,
+                          const void* k, const float* ct, const float* sn, void* q_out, void* k_out,
+                          int64_t tokens, int64_t seq_len, int hq, int hkv, int d, hipStream_t st) {
   const unsigned grid = flat_grid(tokens, 1, kMaxRowGroups);
   auto one = [&](auto w) {
     constexpr int W = decltype(w)::value;
     if (waves != W) return false;
-    rope_tokens<C, CHUNKS, 1, 64 * W><<<grid, 64 * W, 0, st>>>(q, k, ct, sn, q_out, k_out, tokens, seq_len, hq,
-                                                               hkv, d);
+    constexpr auto kernel = rope_tokens<C, CHUNKS, 1, 64 * W>;
+    if (min_rounds > 0) {
+      const int64_t resident = resident_groups<kernel>(64 * W);
+      if (tokens > resident && tokens < min_rounds * resident) return false;
+    }
+    kernel<<<grid, 64 * W, 0, st>>>(q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d);
     return true;
   };
   return (one(std::integral_constant<int, WS>{}) || ...);
@@ -168,14 +176,20 @@ extern "C" int32_t launch_rope_fwd(const void* q, const void* k, const void* cos
     // 52.85 at [16, 1024], 103.55 vs 103.43 at config 4; 64 / 8 heads (576)
     // 25.47 vs 26.29 at [1, 4096], 48.20 vs 49.53 at [1, 8192]; 32 / 32
     // heads (512) 82.62 vs 84.41 at [4, 4096]. Capping these at 4, 5 or 6
-    // workgroups per CU (LDS reserved) measured no different.
+    // workgroups per CU (LDS reserved) measured no different. With 16 chunk
+    // lanes (fp32 head_dim 128: 640 threads for 40 heads) a grid of more
+    // than one and fewer than four rounds of resident workgroups lost to
+    // the 256-thread rounds (9.49 vs 8.71 us at 1024 tokens, 15.79 vs 15.29
+    // at 2048), so those keep them; fewer tokens (2.90 vs 4.05 us at 128,
+    // 5.16 vs 5.79 at 512) and more (103.9 vs 108.4 us at 16384) do not.
     const int heads = hq + hkv;
     const int waves = chunks > 0 ? (heads * chunks + 63) / 64 : 0;
+    using Waves = std::integer_sequence<int, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16>;
     if ((chunks == 8 || chunks == 16) && heads * chunks > 256 && waves <= 16 &&
-        (chunks == 8 ? launch_rope_per_head<C, 8>(waves, std::integer_sequence<int, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16>{},
-                                                  q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d, st)
-                     : launch_rope_per_head<C, 16>(waves, std::integer_sequence<int, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16>{},
-                                                   q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d, st))) {
+        (chunks == 8 ? launch_rope_per_head<C, 8>(waves, 0, Waves{}, q, k, ct, sn, q_out, k_out, tokens, seq_len,
+                                                  hq, hkv, d, st)
+                     : launch_rope_per_head<C, 16>(waves, 4, Waves{}, q, k, ct, sn, q_out, k_out, tokens, seq_len,
+                                                   hq, hkv, d, st))) {
     } else if (chunks == 8) {
       // Tokens of at most 32 heads (and more than 128): with at most 6
       // workgroups per CU (8 fit) this 256-thread shape measured 102.0 vs
