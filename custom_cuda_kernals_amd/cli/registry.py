@@ -309,7 +309,8 @@ REGISTRY: dict[str, OpSpec] = {
             dtypes=("float32", "float16", "bfloat16", "fp8 (gather)"),
             memory_profile="HBM-bound row moves (gather 67 MB, combine k = 2 50 MB at the reference's shapes).",
             design=("four or eight destination rows per gather workgroup; one vector per thread on a flat grid "
-                    "from 2^22 destination vectors", "two expert rows in flight per combine step",
+                    "for rows of more than 512 vectors and from 2^22 destination vectors",
+                    "two expert rows in flight per combine step",
                     "the permutation bookkeeping as one stable counting-sort launch (compute_permutation with "
                     "num_experts)"),
             target="gather and the permutation bit-exact; combine equal to the j-order fp32 sum",

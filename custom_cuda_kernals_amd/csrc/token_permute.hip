@@ -33,35 +33,6 @@ namespace {
 
 #pragma clang fp contract(off)
 
-// Row gather on 16-byte vectors: one workgroup per destination row (grid-
-// stride over rows), VPL vectors per thread per step.
-template <int THREADS, int VPL>
-__global__ __launch_bounds__(THREADS) void token_gather_vec(const u32x4* __restrict__ src,
-                                                            const int64_t* __restrict__ idx,
-                                                            u32x4* __restrict__ dst, int64_t n_dst,
-                                                            int64_t row_vecs, int64_t n_src) {
-  for (int64_t row = blockIdx.x; row < n_dst; row += gridDim.x) {
-    const int64_t s = idx[row];  // workgroup-uniform: one scalar load
-    const bool valid = s >= 0 && s < n_src;
-    const u32x4* sp = src + (valid ? s : 0) * row_vecs;
-    u32x4* dp = dst + row * row_vecs;
-    for (int64_t base = threadIdx.x; base < row_vecs; base += THREADS * VPL) {
-      u32x4 v[VPL];
-#pragma unroll
-      for (int k = 0; k < VPL; ++k) {
-        const int64_t c = base + THREADS * k;
-        v[k] = (u32x4){0u, 0u, 0u, 0u};
-        if (valid && c < row_vecs) v[k] = ld_stream(sp + c);
-      }
-#pragma unroll
-      for (int k = 0; k < VPL; ++k) {
-        const int64_t c = base + THREADS * k;
-        if (c < row_vecs) st_stream(v[k], dp + c);
-      }
-    }
-  }
-}
-
 // Rows of at most THREADS vectors: each workgroup takes R consecutive
 // destination rows per step (grid-stride over groups of R). The R source
 // indices are read first, then every row's vector is in flight at once, so
@@ -411,14 +382,20 @@ inline int32_t elem_bytes(int32_t dtype) {
 // 16384 rows, 191.3 vs 194.7 at 65536 (with the index prefetch below);
 // 1024 -> 2048 rows took 7.5 vs 6.9 us with 8 (a grid of 256 workgroups).
 constexpr int64_t kGatherR8Min = 4096;
-// From 2^22 destination vectors (64 MiB) on, rows of at least 64 vectors take
-// token_gather_flat. Same-run A/B on MI355X, bf16 (fp32) rows, against the
-// row kernels below: 65536 -> 65536 rows of 4096 171.9 vs 190.8 us, 16384
-// rows 43.6 vs 46.8, 8192 rows 23.0 vs 24.0, 32768 rows of 2048 44.1 vs
-// 47.1, 65536 rows of 1024 44.4 vs 47.3, 16384 -> 32768 rows of 7168 149.3
-// vs 152.3; fp32 16384 rows of 4096 85.6 vs 89.1, 65536 rows 348.3 vs 358.7.
-// Below it the row kernels win: 4096 rows of 4096, 11.8 vs 12.6 us;
-// 8192 -> 16384 rows of 1024, 11.8 vs 12.6.
+// Rows of more than 512 vectors take token_gather_flat at every size, and
+// rows of 64 to 512 vectors from 2^22 destination vectors (64 MiB) on.
+// Same-run A/B on MI355X, bf16 (fp32) rows, against the row kernels below
+// (and, past 512 vectors, one 512-thread workgroup per row walking it with
+// one or four vectors per thread in flight): 65536 -> 65536 rows of 4096
+// 171.9 vs 190.8 us, 16384 rows 43.6 vs 46.8, 8192 rows 23.0 vs 24.0, 32768
+// rows of 2048 44.1 vs 47.1, 65536 rows of 1024 44.4 vs 47.3, 16384 -> 32768
+// rows of 7168 149.3 vs 152.3; fp32 16384 rows of 4096 85.6 vs 89.1, 65536
+// rows 348.3 vs 358.7. Past 512 vectors: 256 rows of 7168 3.30 vs 3.84, 2048
+// rows 11.19 vs 11.93, 1024 -> 2048 rows of 11008 15.93 vs 17.09; fp32 512
+// rows of 4096 4.64 vs 4.92, 1024 -> 2048 rows of 7168 19.95 vs 21.39. Up to
+// 512 vectors and below 2^22 the row kernels win: 4096 rows of 4096, 11.6
+// vs 12.1 us; 8192 -> 16384 rows of 1024, 11.8 vs 12.6; 4096 rows of 2048,
+// 6.8 vs 7.4.
 constexpr int64_t kGatherFlatMin = int64_t(1) << 22;
 
 int32_t gather(const void* src, const int64_t* indices, void* dst, int64_t n_dst, int64_t h,
@@ -430,10 +407,10 @@ int32_t gather(const void* src, const int64_t* indices, void* dst, int64_t n_dst
   const int64_t row_bytes = h * es;
   if (row_bytes % 16 == 0 && host_aligned(src, 16) && host_aligned(dst, 16)) {
     const int64_t rv = row_bytes / 16;
-    if (rv >= 64 && n_dst * rv >= kGatherFlatMin) {
+    if (rv > 512 || (rv >= 64 && n_dst * rv >= kGatherFlatMin)) {
       token_gather_flat<<<flat_grid(n_dst * rv, 256, 1 << 20), 256, 0, st>>>(
           static_cast<const u32x4*>(src), indices, static_cast<u32x4*>(dst), n_dst, rv, n_src);
-    } else if (rv <= 512) {
+    } else {
       // One vector per thread, up to 512 threads, R rows per workgroup step:
       // with R = 4, 12.3 vs 12.6 us for one row per workgroup at 2048 -> 4096
       // rows of 8 KB on MI355X (13.0-13.5 with 2-8 vectors per thread).
@@ -460,16 +437,6 @@ int32_t gather(const void* src, const int64_t* indices, void* dst, int64_t n_dst
       } else {
         run(std::integral_constant<int, 4>{});
       }
-    } else if (rv <= 1024) {
-      token_gather_vec<512, 1><<<grid, 512, 0, st>>>(static_cast<const u32x4*>(src), indices,
-                                                    static_cast<u32x4*>(dst), n_dst, rv, n_src);
-    } else {
-      // Rows of more than two 512-vector passes keep four vectors per thread
-      // in flight: 61.9 vs 64.5 us at 2048 -> 4096 fp32 rows of 11008, 31.1 vs
-      // 31.8 in bf16 (one vector per thread stays ahead up to 1024 vectors:
-      // 148.2 vs 149.3-150.6 us at 32768 bf16 rows of 7168).
-      token_gather_vec<512, 4><<<grid, 512, 0, st>>>(static_cast<const u32x4*>(src), indices,
-                                                    static_cast<u32x4*>(dst), n_dst, rv, n_src);
     }
   } else if (es == 4) {
     token_gather_elems<uint32_t><<<grid, 256, 0, st>>>(static_cast<const uint32_t*>(src), indices,

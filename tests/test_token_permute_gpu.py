@@ -71,10 +71,9 @@ def test_gather_vector_tails(dtype):
 def test_gather_row_forms(n_src, n_dst, h, dtype):
     """The gather's launch forms: 4 and 8 rows per workgroup step around 4096
     destination rows, the resident grid with prefetched indices (many short
-    rows), rows of more than 1024 vectors (4 in flight per thread), and the
-    flat form from 2^22 destination vectors (waves that span two rows, a
-    partial last wave, rows of exactly 64 vectors); a few indices out of
-    range in each."""
+    rows), and the flat form (rows of more than 512 vectors at any size, and
+    from 2^22 destination vectors: waves that span two rows, a partial last
+    wave, rows of exactly 64 vectors); a few indices out of range in each."""
     src, idx = inputs.gather_inputs(n_src, n_dst, h, dtype, seed=n_dst + h)
     idx[::997] = n_src  # out of range: zero rows
     out = token_gather(src.cuda(), idx.cuda()).cpu()
