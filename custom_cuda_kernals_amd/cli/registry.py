@@ -246,7 +246,7 @@ REGISTRY: dict[str, OpSpec] = {
             dtypes=("float32", "float16", "bfloat16"),
             memory_profile="HBM-bound: 2 B in + 2 B out per bf16 element plus the tables (config 4: 673 MB).",
             design=("one workgroup per token, a thread per (head, chunk) for 33-128 heads (320 threads at "
-                    "config 4's 40), cos / sin read once per chunk",
+                    "config 4's 40), cos / sin read once per chunk (staged in LDS while the grid fits one round)",
                     "per-token buffer-resource stores with SC1 | NT"),
             target=">= 75 % of 8 TB/s at q [8, 4096, 32, 128] + k [8, 4096, 8, 128] bf16; bit-exact",
             reference=("baselines/rope.py:103-145", "csrc/kernels/rope.cu", "csrc/includes/rope.h:23-36"),

@@ -113,11 +113,79 @@ __global__ __launch_bounds__(256) void rope_scalar(const void* q, const void* k,
   }
 }
 
+// One token per workgroup, a thread per (head, chunk) of it, with the token's
+// cos / sin row loaded once by the first threads and shared through LDS
+// (instead of every thread loading its chunk of both tables). Used where the
+// grid fits one round of resident workgroups; see the launcher.
+template <class C, int CHUNKS, int NT>
+__global__ __launch_bounds__(NT) void rope_heads_staged(const void* q, const void* k,
+                                                        const float* __restrict__ cos_t,
+                                                        const float* __restrict__ sin_t, void* q_out,
+                                                        void* k_out, int64_t tokens, int64_t seq_len,
+                                                        int hq, int hkv, int head_dim) {
+  constexpr int VEC = C::VEC;
+  constexpr int F4 = CHUNKS * VEC / 4;  // float4s in one table row (half = CHUNKS * VEC)
+  __shared__ float4 tab[2 * F4];
+  const int c = threadIdx.x % CHUNKS;
+  const int hh = threadIdx.x / CHUNKS;
+  const int half = head_dim / 2;
+  const int heads = hq + hkv;
+  const bool live = hh < heads;
+  const bool isq = hh < hq;
+  const int idx = live ? (isq ? hh : hh - hq) : 0;  // lanes past the last head read head 0 and store nothing
+  const uint32_t q_bytes = (uint32_t)((int64_t)hq * head_dim * C::kBytes);
+  const uint32_t k_bytes = (uint32_t)((int64_t)hkv * head_dim * C::kBytes);
+  const uint32_t off = (uint32_t)((idx * head_dim + c * VEC) * C::kBytes);
+  for (int64_t tok = blockIdx.x; tok < tokens; tok += gridDim.x) {
+    const int64_t s = tok % seq_len;
+    const char* src = (live && !isq) ? static_cast<const char*>(k) + tok * k_bytes
+                                     : static_cast<const char*>(q) + tok * q_bytes;
+    const u32x4 ra = ld_stream(reinterpret_cast<const u32x4*>(src + off));
+    const u32x4 rb = ld_stream(reinterpret_cast<const u32x4*>(src + off + half * C::kBytes));
+    if (threadIdx.x < 2 * F4) {
+      const float* t = threadIdx.x < F4 ? cos_t : sin_t;
+      tab[threadIdx.x] = reinterpret_cast<const float4*>(t + s * half)[threadIdx.x % F4];
+    }
+    __syncthreads();
+    float cs[VEC], sn[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC / 4; ++i) {
+      const float4 u = tab[c * (VEC / 4) + i], w = tab[F4 + c * (VEC / 4) + i];
+      cs[4 * i] = u.x; cs[4 * i + 1] = u.y; cs[4 * i + 2] = u.z; cs[4 * i + 3] = u.w;
+      sn[4 * i] = w.x; sn[4 * i + 1] = w.y; sn[4 * i + 2] = w.z; sn[4 * i + 3] = w.w;
+    }
+    float x1[VEC], x2[VEC], o1[VEC], o2[VEC];
+    C::unpack(ra, x1);
+    C::unpack(rb, x2);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      o1[i] = x1[i] * cs[i] - x2[i] * sn[i];
+      o2[i] = x2[i] * cs[i] + x1[i] * sn[i];
+    }
+    if (live) {
+      if (isq) {
+        const RopeRow<1> qo(static_cast<char*>(q_out) + tok * q_bytes, q_bytes);
+        qo.st16(C::pack(o1), off);
+        qo.st16(C::pack(o2), off + half * C::kBytes);
+      } else {
+        const RopeRow<1> ko(static_cast<char*>(k_out) + tok * k_bytes, k_bytes);
+        ko.st16(C::pack(o1), off);
+        ko.st16(C::pack(o2), off + half * C::kBytes);
+      }
+    }
+    __syncthreads();  // the next token rewrites tab
+  }
+}
+
 // One token per workgroup of 64 * W threads for the W in WS that equals
 // `waves`: a thread per (head, chunk) of the token, so no thread rotates a
-// second head after its first. With min_rounds > 0, not when the tokens
-// fill more than one but fewer than min_rounds rounds of the workgroups the
-// device holds at once. false (nothing launched) otherwise.
+// second head after its first. Up to one round of the workgroups the device
+// holds at once the tables are staged in LDS (rope_heads_staged): 3.51 vs
+// 3.95 us at 512 tokens of 32 / 8 heads of 128 bf16, 5.13 vs 5.61 at 1024;
+// with more tokens the per-token barrier lost (15.75 vs 15.29 us at 4096,
+// 105.4 vs 103.2 at config 4). With min_rounds > 0, not when the tokens fill
+// more than one but fewer than min_rounds rounds. false (nothing launched)
+// otherwise.
 template <class C, int CHUNKS, int... WS>
 bool launch_rope_per_head(int waves, int min_rounds, std::integer_sequence<int, WS...>, const void* q,
                           const void* k, const float* ct, const float* sn, void* q_out, void* k_out,
@@ -126,6 +194,11 @@ bool launch_rope_per_head(int waves, int min_rounds, std::integer_sequence<int, 
   auto one = [&](auto w) {
     constexpr int W = decltype(w)::value;
     if (waves != W) return false;
+    constexpr auto staged = rope_heads_staged<C, CHUNKS, 64 * W>;
+    if (tokens <= resident_groups<staged>(64 * W)) {
+      staged<<<grid, 64 * W, 0, st>>>(q, k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d);
+      return true;
+    }
     constexpr auto kernel = rope_tokens<C, CHUNKS, 1, 64 * W>;
     if (min_rounds > 0) {
       const int64_t resident = resident_groups<kernel>(64 * W);

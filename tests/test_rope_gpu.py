@@ -25,7 +25,9 @@ CASES = [(4, 128, 12, 12, 64), (2, 2048, 32, 8, 128), (1, 4096, 32, 8, 128), (3,
          # a thread per (head, chunk) in workgroups of 5-16 waves: 72, 64, 33 and 128 heads of 128 (8 chunk
          # lanes; fp32 16: 1152 threads fall back to rounds), 48 and 129 heads of 64 (fp32: 8 chunk lanes)
          (1, 64, 64, 8, 128), (2, 33, 32, 32, 128), (1, 50, 29, 4, 128), (1, 20, 120, 8, 128), (3, 7, 40, 8, 64),
-         (1, 9, 100, 29, 64)]
+         (1, 9, 100, 29, 64),
+         # up to one round of resident workgroups the tables are staged in LDS (1024 tokens), beyond it not
+         (1, 1024, 32, 8, 128)]
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
 
 
