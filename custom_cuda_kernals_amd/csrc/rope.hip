@@ -13,7 +13,9 @@
 // first, then k heads) with a stride of the number of head lanes, so its
 // cos/sin chunk is loaded once per token and reused for every head it takes.
 // Workgroups are 256 threads, or, for one token of more heads than 256
-// threads cover at once, a thread per (head, chunk) of the token.
+// threads cover at once, a thread per (head, chunk) of the token; while the
+// grid fits one round of resident workgroups, a thread per (head, chunk)
+// with the token's cos/sin row staged in LDS.
 // All accesses are 16 bytes; a wave covers whole 128-byte cache lines.
 #include "launch.hpp"
 
@@ -210,6 +212,30 @@ bool launch_rope_per_head(int waves, int min_rounds, std::integer_sequence<int, 
   return (one(std::integral_constant<int, WS>{}) || ...);
 }
 
+// Tokens of at most 256 / CHUNKS heads while the grid fits one round of the
+// workgroups the device holds at once: rope_heads_staged in one workgroup of
+// 64 * W threads (W in WS equal to `waves`). false (nothing launched)
+// otherwise. Same-run A/B on MI355X against the 256-thread workgroups below,
+// bf16: 28 / 4 heads of 128 at 512 tokens 3.24 vs 3.86 us, 1024 4.64 vs
+// 5.34; 12 / 12 heads of 64 at 512 tokens 2.69 vs 3.33 (fp32 2.94 vs 3.38);
+// 16 / 16 heads of 64 at 1024 3.55 vs 3.79; 8 / 8 heads of 128 at 256
+// tokens 2.54 vs 2.50 (fp32 2.73 vs 2.60).
+template <class C, int CHUNKS, int... WS>
+bool launch_rope_staged_small(int waves, std::integer_sequence<int, WS...>, const void* q, const void* k,
+                              const float* ct, const float* sn, void* q_out, void* k_out, int64_t tokens,
+                              int64_t seq_len, int hq, int hkv, int d, hipStream_t st) {
+  auto one = [&](auto w) {
+    constexpr int W = decltype(w)::value;
+    if (waves != W) return false;
+    constexpr auto staged = rope_heads_staged<C, CHUNKS, 64 * W>;
+    if (tokens > resident_groups<staged>(64 * W)) return false;
+    staged<<<flat_grid(tokens, 1, kMaxRowGroups), 64 * W, 0, st>>>(q, k, ct, sn, q_out, k_out, tokens, seq_len,
+                                                                    hq, hkv, d);
+    return true;
+  };
+  return (one(std::integral_constant<int, WS>{}) || ...);
+}
+
 }  // namespace
 }  // namespace cck
 
@@ -263,6 +289,14 @@ extern "C" int32_t launch_rope_fwd(const void* q, const void* k, const void* cos
                                                   hq, hkv, d, st)
                      : launch_rope_per_head<C, 16>(waves, 4, Waves{}, q, k, ct, sn, q_out, k_out, tokens, seq_len,
                                                    hq, hkv, d, st))) {
+    } else if (heads * chunks <= 256 &&
+               ((chunks == 8 && launch_rope_staged_small<C, 8>(waves, std::integer_sequence<int, 1, 2, 3, 4>{}, q, k,
+                                                                ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d, st)) ||
+                (chunks == 4 && launch_rope_staged_small<C, 4>(waves, std::integer_sequence<int, 1, 2, 3, 4>{}, q, k,
+                                                                ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d, st)) ||
+                (chunks == 16 && launch_rope_staged_small<C, 16>(waves, std::integer_sequence<int, 1, 2, 3, 4>{}, q,
+                                                                  k, ct, sn, q_out, k_out, tokens, seq_len, hq, hkv, d,
+                                                                  st)))) {
     } else if (chunks == 8) {
       // Tokens of at most 32 heads (and more than 128): with at most 6
       // workgroups per CU (8 fit) this 256-thread shape measured 102.0 vs
