@@ -127,6 +127,7 @@ __global__ __launch_bounds__(NT) void rope_heads_staged(const void* q, const voi
                                                         int hq, int hkv, int head_dim) {
   constexpr int VEC = C::VEC;
   constexpr int F4 = CHUNKS * VEC / 4;  // float4s in one table row (half = CHUNKS * VEC)
+  static_assert(2 * F4 <= NT, "the first 2 * F4 threads load the cos and sin rows");
   __shared__ float4 tab[2 * F4];
   const int c = threadIdx.x % CHUNKS;
   const int hh = threadIdx.x / CHUNKS;
