@@ -113,6 +113,35 @@ def test_swiglu_fp8_parked_row_edges(shape):
     _check_swiglu(g, u, "e4m3", None)
 
 
+def _nan_aware_equal(got: np.ndarray, want: np.ndarray, nan_of) -> None:
+    """Equal bit for bit, except that NaNs (as `nan_of` tells them) only need
+    to be NaN on both sides: the sign of a NaN is not pinned (see the test
+    below)."""
+    gn, wn = nan_of(got), nan_of(want)
+    assert np.array_equal(gn, wn), "NaN positions differ"
+    assert np.array_equal(got[~wn], want[~wn]), "non-NaN values differ"
+
+
+@pytest.mark.parametrize("shape", [(1200, 12288), (64, 4096)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_rmsnorm_fp8_non_finite_rows(shape):
+    """Per-token RMSNorm + FP8 with NaN and infinite inputs / residuals in a few
+    rows (rows looping on a resident grid, and one workgroup per row): codes,
+    scales and residual_out equal the composed eager oracle bit for bit, NaNs
+    compared as NaN."""
+    x, r, w = inputs.rmsnorm_inputs(*shape, torch.bfloat16, seed=shape[1] + 11)
+    x[2, 7] = float("nan")
+    r[4, 100] = float("inf")
+    x[6, 3] = float("-inf")
+    q, s, ro = rmsnorm_residual_fp8(x.cuda(), r.cuda(), w.cuda(), 1e-5, fp8_format="e4m3")
+    strict, s_ref, ro_ref, _ = eager.rmsnorm_residual_fp8(x, r, w, 1e-5, "e4m3", None)
+    _nan_aware_equal(codes_np(q).reshape(strict.shape), strict, lambda c: (c & 0x7F) == 0x7F)
+    _nan_aware_equal(s.cpu().numpy().view(np.uint32), np.asarray(s_ref, dtype=np.float32).reshape(-1).view(np.uint32),
+                     lambda b: (b & 0x7FFFFFFF) > 0x7F800000)
+    _nan_aware_equal(ro.cpu().view(torch.int16).numpy(), ro_ref.view(torch.int16).numpy(),
+                     lambda b: (b & 0x7FFF) > 0x7F80)
+    assert ((codes_np(q).reshape(strict.shape) & 0x7F) == 0x7F).any(axis=1).sum() >= 3
+
+
 @pytest.mark.parametrize("shape", [(600, 22528), (64, 14336)], ids=lambda s: f"{s[0]}x{s[1]}")
 def test_swiglu_fp8_non_finite_rows(shape):
     """Per-token SwiGLU + FP8 with NaN and infinite gates / ups in a few rows
